@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A8 quantized linear path on one MI355X.
+
+Headline (value): weight-stream GB/s of the decode GEMV at M=1 over one Qwen3-4B
+decoder layer's four projections (qkv 2560->6144, o 4096->2560, gate_up
+2560->19456 with the SiLU-gate epilogue, down 9728->2560), W4 codes packed two per
+byte.  One step = those four linears of one layer, each a single launch that
+quantizes its fp16 input row itself.  The steps rotate over 36 distinct layer copies
+(1.82 GB of weights), so the 256 MB Infinity Cache cannot hold the stream.
+Bytes per step = packed codes + f32 scales = 50,585,600.
+
+Also reported: the dominant kernel's roofline (the gate_up GEMV, HIP events on the
+launch stream), int8 TOPS of the M=512 prefill GEMMs of the same layer, and the
+CPU oracle timed on the host cores over a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--prefill-reps R]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published (5.0 POPS)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--kernel-reps", type=int, default=1000)
+    ap.add_argument("--prefill-reps", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded "
+              "across GPUs in this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from open_rknpu2_lm_infer_amd import _lib
+    from open_rknpu2_lm_infer_amd import qlinear as ql
+    from open_rknpu2_lm_infer_amd import synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    info = _lib.device_info(0)
+    log(f"device: {torch.cuda.get_device_name(0)} CUs={info.cu_count} sclk={info.sclk_khz / 1e3:.0f} MHz")
+
+    # ---------------------------------------------------------------- weights (resident)
+    L = args.layers
+    layers = []
+    codes0 = []  # host copy of layer 0 for the CPU baseline
+    t0 = time.time()
+    for l in range(L):
+        projs = []
+        for p, (name, K, N) in enumerate(synth.LAYER):
+            packed, codes, sc = synth.make_linear(N, K, 4, synth.linear_seed(l, p), device=dev)
+            projs.append(ql.Weights.from_packed_device(4, K, N, packed, sc))
+            if l == 0:
+                codes0.append((codes.cpu().numpy(), sc.cpu().numpy()))
+            del packed, codes, sc
+        layers.append(projs)
+    torch.cuda.synchronize()
+    log(f"{L} layers of W4 weights resident ({time.time() - t0:.1f} s)")
+
+    bytes_layer = sum(w.N * w.K // 2 + w.N * 4 for w in layers[0])
+    ws = ql.Workspace(512, 9728, 19456)
+    acts = [synth.activations(1, K, seed=synth.linear_seed(0, p) + 1, device=dev)
+            for p, (_, K, _) in enumerate(synth.LAYER)]
+    outs = [torch.empty((1, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+            for name, K, N in synth.LAYER]
+    flags = [ql.QLIN_SWIGLU if name == "gate_up" else 0 for name, _, _ in synth.LAYER]
+
+    def step(i):
+        projs = layers[i % L]
+        for p in range(4):
+            ql.run(ws, projs[p], acts[p], out=outs[p], flags=flags[p])
+
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def capture(fn, count):
+        """HIP graph of fn(0..count-1); launches happen on torch's capture stream."""
+        for i in range(min(count, 4)):
+            fn(i)  # eager first: code objects load outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(count):
+                fn(i)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, reps):
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3  # seconds
+
+    # ---------------------------------------------------------------- headline: decode layer
+    # One graph = one pass over the L resident layers (4 launches each); the timed
+    # region replays it until `steps` layer-steps have run.
+    g_layers = capture(step, L)
+    reps_w = max(1, -(-args.warmup // L))
+    time_graph(g_layers, reps_w)
+    log(f"warmup {reps_w * L} steps done")
+    reps = max(1, -(-args.steps // L))
+    steps = reps * L
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sec = time_graph(g_layers, reps)
+    wall = time.perf_counter() - t0
+    ms_per_step = sec * 1e3 / steps
+    value = bytes_layer * steps / sec / 1e9
+    log(f"decode layer (graph): {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s (wall {wall:.3f} s)")
+    # eager launches of the same step, for reference (host launch rate bound)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for i in range(200):
+        step(i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    eager_us = e0.elapsed_time(e1) * 1e3 / 200
+    log(f"decode layer (eager launches): {eager_us:.2f} us/step")
+
+    # ---------------------------------------------------------------- per-kernel (graph, events)
+    per_kernel = {}
+    for p, (name, K, N) in enumerate(synth.LAYER):
+        g = capture(lambda i, p=p: ql.run(ws, layers[i % L][p], acts[p], out=outs[p], flags=flags[p]), L)
+        r = max(1, args.kernel_reps // L)
+        us = time_graph(g, r) * 1e6 / (r * L)
+        b = N * K // 2 + N * 4
+        per_kernel[name] = {"us": round(us, 3), "bytes": b, "gbs": round(b / (us * 1e-6) / 1e9, 1)}
+        log(f"  gemv {name}: {us:.2f} us/launch, {per_kernel[name]['gbs']} GB/s")
+        del g
+    dom = per_kernel["gate_up"]
+
+    # ---------------------------------------------------------------- prefill GEMM M=512
+    M = 512
+    pre_acts = [synth.activations(M, K, seed=synth.linear_seed(0, p) + 2, device=dev)
+                for p, (_, K, _) in enumerate(synth.LAYER)]
+    pre_outs = [torch.empty((M, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+                for name, K, N in synth.LAYER]
+    prefill = {}
+    tot_ops, tot_us = 0.0, 0.0
+    for p, (name, K, N) in enumerate(synth.LAYER):
+        g = capture(lambda i, p=p: ql.run(ws, layers[i % L][p], pre_acts[p], out=pre_outs[p], flags=flags[p]), L)
+        r = max(1, args.prefill_reps)
+        us = time_graph(g, r) * 1e6 / (r * L)
+        ops = 2.0 * M * N * K
+        tot_ops += ops
+        tot_us += us
+        prefill[name] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+        log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM)")
+        del g
+    prefill_tops = tot_ops / (tot_us * 1e-6) / 1e12
+
+    # ---------------------------------------------------------------- CPU oracle baseline
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        a_host = [a.cpu().numpy().view(np.uint16) for a in acts]
+        n_layers, t0 = 0, time.perf_counter()
+        while True:
+            for p, (name, K, N) in enumerate(synth.LAYER):
+                orc.linear_f16(a_host[p], codes0[p][0], codes0[p][1], swiglu=(name == "gate_up"),
+                               threads=threads)
+            n_layers += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds:
+                break
+        cpu_gbs = bytes_layer * n_layers / el / 1e9
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{n_layers} passes of the same M=1 W4 layer (4 linears, fp16 in/out) in "
+                         f"{el:.1f} s with the C oracle (OpenMP, int8 codes unpacked in host memory)"}
+        log(f"cpu baseline: {cpu_gbs:.2f} GB/s on {threads} threads")
+
+    result = {
+        "metric": "weight-stream GB/s @M=1 + int8 TOPS @M=512, Qwen3-4B W4A8 linears",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "eager_us_per_step": round(eager_us, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded: W4 codes U[-8,7], scales U(0.01,0.1), fp16 N(0,1) activations with 1% x20 outlier channels)",
+        "config": {
+            "workload": "W4A8 decode GEMV over one Qwen3-4B layer (qkv 2560x6144, o 4096x2560, "
+                        "gate_up 2560x19456 + SiLU-gate, down 9728x2560), M=1, fp16 in/out, "
+                        f"{L} layer copies rotated",
+            "rows": 1,
+            "bytes_per_step": bytes_layer,
+            "layers_rotated": L,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv gate_up (W4, SiLU-gate epilogue, fused quant)",
+            "achieved": dom["gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "per_kernel_decode": per_kernel,
+        "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
+                         "per_proj": prefill},
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,189 @@
+/*
+ * qlinear.h - C ABI of the MI355X (gfx950) W4A8 / W8A8 quantized linear.
+ *
+ * Symmetric per-output-channel int4/int8 weights times dynamic per-token int8
+ * activations, as used by every Q/K/V/O and gate/up/down projection of the
+ * HC-Zhou/open_rknpu2_lm_infer engine.  Each entry point below names the native
+ * library call of the reference it replaces; the reference reaches those through
+ * bindgen (build.rs:44-67) and calls them from src/npu.rs.
+ *
+ * Arithmetic (identical to the reference oracle, src/npu.rs:1097-1121):
+ *   s[m]    = absmax_k |A[m,k]| == 0 ? 1 : max(absmax/127, FLT_MIN)
+ *   q[m,k]  = clamp(round(A[m,k] * (1/s[m])), -127, 127)   round = half away from zero
+ *   acc     = sum_k q[m,k] * codes[k,n]                      exact int32
+ *   C[m,n]  = (float(acc) * s[m]) * scales[n]
+ *   SwiGLU: C[m,j] = (g/(1+exp(-g))) * u, g = col j, u = col j + N/2 (src/npu.rs:1202-1208)
+ *
+ * Conventions: functions return 0 (QLIN_OK) or a negative QLIN_ERR_* code;
+ * qlin_strerror() names it.  Handles are opaque and owned by the caller, who
+ * frees them with the paired *_free.  Host buffers passed to *_create are copied.
+ * Entry points taking `stream` are asynchronous and stream-ordered (stream is a
+ * hipStream_t, NULL = default stream); pointers passed to them are device
+ * pointers.  One workspace must not be used by two streams at once.
+ */
+#ifndef QLINEAR_H
+#define QLINEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- return codes (src/npu.rs:138-151 maps them through rk_npu_strerror) ---- */
+#define QLIN_OK 0
+#define QLIN_ERR_PARAM (-1)       /* invalid argument, like RK_NPU_ERR_PARAM */
+#define QLIN_ERR_NOMEM (-2)       /* device or pinned host allocation failed */
+#define QLIN_ERR_DEVICE (-3)      /* a HIP runtime call failed */
+#define QLIN_ERR_NONFINITE (-4)   /* activation row holds Inf/NaN (the native library rejects it) */
+#define QLIN_ERR_UNSUPPORTED (-5) /* shape not supported by this entry point */
+#define QLIN_ERR_NODEVICE (-6)    /* no gfx950 device visible */
+
+/* ---- element types of activations / outputs ---- */
+#define QLIN_F32 0
+#define QLIN_F16 1
+
+/* ---- flags ---- */
+#define QLIN_ROUND_HALF_EVEN 0x1u /* q rounding half to even; default is half away (Rust f32::round) */
+#define QLIN_NORM_SEQUENTIAL 0x2u /* RMSNorm sum order of src/ops/norm.rs:23-48 instead of the
+                                     16-accumulator order of src/model/cpu.rs:11-41 */
+#define QLIN_SWIGLU 0x4u          /* fused SiLU(gate)*up epilogue, output [M, N/2] */
+#define QLIN_NO_FUSED_QUANT 0x8u  /* decode: quantize in a separate launch instead of in the GEMV */
+
+typedef struct qlin_weights qlin_weights;
+typedef struct qlin_workspace qlin_workspace;
+
+/* Geometry of one linear (reference: rk_npu_i4_weight_config {K, N, k_tile} and
+ * rk_npu_matmul_weight_config, src/npu.rs:392-396,432-436). */
+typedef struct qlin_weight_config {
+    int32_t bits; /* 4 or 8 */
+    int32_t K;    /* in-features, 1..2^30 */
+    int32_t N;    /* out-features, 1..2^30 */
+} qlin_weight_config;
+
+/* Reference: rk_npu_w4a8_weight_info / rk_npu_i4_weights_memory_query (src/npu.rs:408-423). */
+typedef struct qlin_weight_info {
+    int32_t bits, K, N;
+    int32_t K_padded;      /* K rounded up to 128 (zero codes in the pad) */
+    int32_t N_padded;      /* N rounded up to 64 (zero codes and scales in the pad) */
+    int32_t device;        /* HIP device ordinal holding the weights */
+    uint64_t device_bytes; /* packed codes + scales resident in HBM */
+} qlin_weight_info;
+
+/* Reference: rk_npu_w4a8_memory_info_ex / rk_npu_matmul_workspace_requirements (src/npu.rs:955-986). */
+typedef struct qlin_workspace_info {
+    int32_t max_rows;
+    int32_t reserved;
+    uint64_t device_bytes;      /* scratch: quantized rows, scales, split-K partials, counters */
+    uint64_t pinned_host_bytes; /* staging for the host-buffer entry points */
+} qlin_workspace_info;
+
+/* Reference: rk_npu_strerror (src/npu.rs:138-144). */
+const char* qlin_strerror(int rc);
+
+/* Device and build facts used for roofline reporting: CU count, peak shader clock
+ * (kHz), HBM bus width (bits), memory clock (kHz), and gfx arch number (950). */
+typedef struct qlin_device_info {
+    int32_t device, cu_count, arch, reserved;
+    int64_t sclk_khz, mclk_khz, bus_width_bits, hbm_bytes;
+} qlin_device_info;
+int qlin_device_query(int32_t device, qlin_device_info* out);
+
+/* ---- weights ----
+ * Replaces rk_npu_w4a8_weights_create (W4, src/npu.rs:397-405) and
+ * rk_npu_f32i8f32_weights_create (W8, src/npu.rs:439-447).  codes are the
+ * reference QuantMatrix layout: int8 [K, N] K-major, codes[k*N + n], values in
+ * [-8, 7] for bits = 4 and [-127, 127] for bits = 8; scales f32 [N], positive.
+ * Both are host pointers, copied into the current HIP device's HBM as
+ * [N, K/2] nibble-packed (low nibble = even k) or [N, K] int8.  Out-of-range
+ * codes or non-positive / non-finite scales return QLIN_ERR_PARAM. */
+int qlin_weights_create(const qlin_weight_config* config, const int8_t* codes_kn,
+                        const float* scales, qlin_weights** out);
+
+/* Same, from the device layout directly (host pointers): packed is [N, K/2] bytes
+ * with the low nibble holding the even k (bits = 4, K even) or [N, K] int8
+ * (bits = 8).  Used by the compressed-tensors loader and the benchmark. */
+int qlin_weights_create_packed(const qlin_weight_config* config, const void* packed_nk,
+                               const float* scales, qlin_weights** out);
+
+/* Same as qlin_weights_create_packed, but packed_nk and scales are DEVICE pointers
+ * (copied device-to-device on `stream`); no host round trip for large stacks. */
+int qlin_weights_create_packed_device(const qlin_weight_config* config, const void* packed_nk,
+                                      const float* scales, void* stream, qlin_weights** out);
+
+/* Replaces rk_npu_w4a8_weights_free / rk_npu_f32i8f32_weights_free (src/npu.rs:411,452). */
+void qlin_weights_free(qlin_weights* weights);
+
+/* Replaces rk_npu_w4a8_weights_query + rk_npu_i4_weights_memory_query (src/npu.rs:407-423). */
+int qlin_weights_query(const qlin_weights* weights, qlin_weight_info* out);
+
+/* ---- workspace ----
+ * Replaces rk_npu_w4a8_workspace_create_ex / rk_npu_matmul_workspace_create
+ * (src/npu.rs:964-991).  A workspace serves any weights with K <= max_k and
+ * N <= max_n, at 1..max_rows rows.  The reference fixes M per workspace (its
+ * bucket(), src/npu.rs:152-162); here any rows <= max_rows run. */
+int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_workspace** out);
+void qlin_workspace_free(qlin_workspace* ws);
+int qlin_workspace_query(const qlin_workspace* ws, qlin_workspace_info* out);
+
+/* Sticky error word of asynchronous runs on this workspace: returns QLIN_OK or
+ * QLIN_ERR_NONFINITE if any activation row seen since the last clear held Inf/NaN.
+ * Synchronizes the workspace's last stream.  clear != 0 resets it. */
+int qlin_workspace_status(qlin_workspace* ws, int32_t clear);
+
+/* ---- host-buffer runs: the drop-in for the reference's synchronous calls ----
+ * Replaces rk_npu_w4a8_run_f32 (src/npu.rs:1047-1049) and rk_npu_f32i8f32_run_dynamic
+ * (src/npu.rs:1052-1061): A f32 [rows, K] and C f32 [rows, N] are host pointers;
+ * the call returns after C is written.  Non-finite input returns QLIN_ERR_NONFINITE. */
+int qlin_run_f32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, const float* A,
+                 float* C);
+
+/* Replaces rk_npu_w4a8_run_swiglu_f32 (src/npu.rs:1044-1046): C is [rows, N/2].
+ * Needs N % 64 == 0 (the reference's own condition, src/npu.rs:1011); otherwise
+ * returns QLIN_ERR_UNSUPPORTED and the caller runs qlin_run_f32 + its own SwiGLU,
+ * as the reference caller does when run_swiglu returns false. */
+int qlin_run_swiglu_f32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
+                        const float* A, float* C);
+
+/* ---- device runs (MI355X-native, asynchronous) ----
+ * A: device [rows, lda] of a_dtype; C: device [rows, ldc] of c_dtype, N columns
+ * (N/2 with QLIN_SWIGLU).  flags: QLIN_ROUND_HALF_EVEN, QLIN_SWIGLU,
+ * QLIN_NO_FUSED_QUANT.  Non-finite input sets the workspace's sticky error. */
+int qlin_run(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, const void* A,
+             int32_t a_dtype, int64_t lda, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags,
+             void* stream);
+
+/* RMSNorm -> quantize -> linear in one call (src/model/dense.rs:416-430,486-505:
+ * Cpu::norm then Projection::run).  gamma: device f32 [K]; eps > 0.  The norm
+ * output stays in f32 registers and is never rounded to fp16 before quantization,
+ * as in the reference where norm_row writes f32.  flags as qlin_run plus
+ * QLIN_NORM_SEQUENTIAL. */
+int qlin_run_rmsnorm(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
+                     const void* A, int32_t a_dtype, int64_t lda, const float* gamma, float eps,
+                     void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream);
+
+/* ---- stage entry points (parity checks and composition) ----
+ * Per-token quantization alone (the library's scan + quantize,
+ * QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:26-27).  q: device int8 [rows, ldq], the
+ * K..ldq-1 tail zero-filled; s: device f32 [rows].  gamma != NULL applies RMSNorm
+ * first.  err (device uint32, may be NULL) gets bit 0 set on non-finite input. */
+int qlin_quantize(int32_t rows, int32_t K, const void* A, int32_t a_dtype, int64_t lda,
+                  const float* gamma, float eps, int8_t* q, int64_t ldq, float* s, uint32_t* err,
+                  uint32_t flags, void* stream);
+
+/* Exact int32 acc[rows, ldacc] = q[rows, :K] x codes over the whole N (the library's
+ * integer GEMM + reduce, PIPELINE_REVIEW:28-30).  q: device int8 [rows, ldq] with
+ * ldq >= K_padded and zeros in [K, K_padded). */
+int qlin_gemm_i32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, const int8_t* q,
+                  int64_t ldq, int32_t* acc, int64_t ldacc, void* stream);
+
+/* Linear from already-quantized rows: the epilogue applies (float(acc)*s[m])*scales[n]
+ * (and SwiGLU with QLIN_SWIGLU).  Lets a producer kernel hand over q and s directly. */
+int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
+                       const int8_t* q, int64_t ldq, const float* s, void* C, int32_t c_dtype,
+                       int64_t ldc, uint32_t flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QLINEAR_H */

@@ -1,0 +1,564 @@
+// C ABI of libqlinear: weights, workspaces, dispatch between the decode GEMV and the
+// prefill GEMM, and the host-buffer entry points that mirror the reference's
+// synchronous rk_npu_w4a8_run_f32 / rk_npu_f32i8f32_run_dynamic.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/qlinear.h"
+#include "qlin_internal.hpp"
+
+namespace qlin {
+size_t gemv_lds_bytes_for(int M, int steps_per_split, int bits);
+}
+
+using namespace qlin;
+
+struct qlin_weights {
+    int bits, K, N, Kp, Np, device;
+    int64_t wrow;  // bytes per row
+    uint8_t* W;
+    float* scales;
+};
+
+struct qlin_workspace {
+    int max_rows, max_k, max_n, max_kp, max_np, device, cu_count;
+    int8_t* q;           // [max_rows, max_kp]
+    float* s;            // [max_rows]
+    int32_t* gemv_part;  // [kGemvMaxRows, max_np], zero at rest
+    uint32_t* counters;  // [n_counters], zero at rest
+    int n_counters;
+    int32_t* gemm_part;  // [kGemmPartTiles * 64 * 256]
+    uint32_t* err;       // sticky error word
+    float* dA;           // host-API staging [max_rows, max_k]
+    float* dC;           // host-API staging [max_rows, max_n]
+    hipStream_t stream;  // stream of the host-buffer entry points
+    hipStream_t last;    // stream of the most recent run
+    uint64_t device_bytes;
+};
+
+namespace {
+
+constexpr int kGemmPartTiles = 512;  // max tiles x splits of one split-K launch
+constexpr int kGemmTile = 128;
+
+int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
+int current_device(int* dev) { return hipGetDevice(dev) == hipSuccess ? QLIN_OK : QLIN_ERR_NODEVICE; }
+
+int cu_count(int dev) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    return n;
+}
+
+__global__ void pack_kn_kernel(const int8_t* codes, int K, int N, int Kp, int Np, int bits, uint8_t* out) {
+    const int64_t row_bytes = bits == 4 ? Kp / 2 : Kp;
+    const int64_t total = (int64_t)Np * row_bytes;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int n = (int)(i / row_bytes);
+        const int j = (int)(i - (int64_t)n * row_bytes);
+        if (bits == 8) {
+            const int k = j;
+            out[i] = (n < N && k < K) ? (uint8_t)codes[(int64_t)k * N + n] : 0;
+        } else {
+            const int k = 2 * j;
+            const int lo = (n < N && k < K) ? codes[(int64_t)k * N + n] : 0;
+            const int hi = (n < N && k + 1 < K) ? codes[(int64_t)(k + 1) * N + n] : 0;
+            out[i] = (uint8_t)((lo & 0xf) | ((hi & 0xf) << 4));
+        }
+    }
+}
+
+int check_config(const qlin_weight_config* c) {
+    if (!c || (c->bits != 4 && c->bits != 8) || c->K <= 0 || c->N <= 0 || c->K > kMaxK ||
+        c->N > (1 << 30))
+        return QLIN_ERR_PARAM;
+    return QLIN_OK;
+}
+
+int check_scales(const float* scales, int N) {
+    if (!scales) return QLIN_ERR_PARAM;
+    for (int n = 0; n < N; ++n)
+        if (!(scales[n] > 0.0f) || !std::isfinite(scales[n])) return QLIN_ERR_PARAM;
+    return QLIN_OK;
+}
+
+int alloc_weights(const qlin_weight_config* c, qlin_weights** w) {
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    auto* x = new (std::nothrow) qlin_weights();
+    if (!x) return QLIN_ERR_NOMEM;
+    x->bits = c->bits;
+    x->K = c->K;
+    x->N = c->N;
+    x->Kp = (int)round_up(c->K, kKAlign);
+    x->Np = (int)round_up(c->N, kNAlign);
+    x->device = dev;
+    x->wrow = c->bits == 4 ? x->Kp / 2 : x->Kp;
+    if (hipMalloc(&x->W, (size_t)x->Np * x->wrow) != hipSuccess ||
+        hipMalloc(&x->scales, (size_t)x->Np * sizeof(float)) != hipSuccess) {
+        (void)hipFree(x->W);
+        (void)hipFree(x->scales);
+        delete x;
+        return QLIN_ERR_NOMEM;
+    }
+    *w = x;
+    return QLIN_OK;
+}
+
+int upload_scales(qlin_weights* x, const float* scales, hipMemcpyKind kind, hipStream_t st) {
+    if (hipMemsetAsync(x->scales, 0, (size_t)x->Np * sizeof(float), st) != hipSuccess ||
+        hipMemcpyAsync(x->scales, scales, (size_t)x->N * sizeof(float), kind, st) != hipSuccess)
+        return QLIN_ERR_DEVICE;
+    return QLIN_OK;
+}
+
+bool gemv_ok(const qlin_workspace* ws, const qlin_weights* w, int rows) {
+    (void)ws;
+    (void)w;
+    return rows <= kGemvMaxRows;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qlin_strerror(int rc) {
+    switch (rc) {
+        case QLIN_OK: return "success";
+        case QLIN_ERR_PARAM: return "invalid parameter";
+        case QLIN_ERR_NOMEM: return "out of device or host memory";
+        case QLIN_ERR_DEVICE: return "HIP runtime error";
+        case QLIN_ERR_NONFINITE: return "non-finite activation";
+        case QLIN_ERR_UNSUPPORTED: return "shape not supported by this entry point";
+        case QLIN_ERR_NODEVICE: return "no HIP device";
+        default: return "unknown error";
+    }
+}
+
+int qlin_device_query(int32_t device, qlin_device_info* out) {
+    if (!out) return QLIN_ERR_PARAM;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return QLIN_ERR_NODEVICE;
+    std::memset(out, 0, sizeof(*out));
+    out->device = device;
+    out->cu_count = prop.multiProcessorCount;
+    out->sclk_khz = prop.clockRate;
+    out->mclk_khz = prop.memoryClockRate;
+    out->bus_width_bits = prop.memoryBusWidth;
+    out->hbm_bytes = (int64_t)prop.totalGlobalMem;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) out->arch = 950;
+    return QLIN_OK;
+}
+
+int qlin_weights_create(const qlin_weight_config* config, const int8_t* codes_kn, const float* scales,
+                        qlin_weights** out) {
+    if (!out) return QLIN_ERR_PARAM;
+    *out = nullptr;
+    if (int rc = check_config(config)) return rc;
+    if (!codes_kn) return QLIN_ERR_PARAM;
+    if (int rc = check_scales(scales, config->N)) return rc;
+    const int64_t total = (int64_t)config->K * config->N;
+    const int lo = config->bits == 4 ? -8 : -127, hi = config->bits == 4 ? 7 : 127;
+    for (int64_t i = 0; i < total; ++i)
+        if (codes_kn[i] < lo || codes_kn[i] > hi) return QLIN_ERR_PARAM;
+    qlin_weights* w = nullptr;
+    if (int rc = alloc_weights(config, &w)) return rc;
+    int8_t* staging = nullptr;
+    int rc = QLIN_OK;
+    if (hipMalloc(&staging, (size_t)total) != hipSuccess) rc = QLIN_ERR_NOMEM;
+    if (!rc && hipMemcpy(staging, codes_kn, (size_t)total, hipMemcpyHostToDevice) != hipSuccess) rc = QLIN_ERR_DEVICE;
+    if (!rc) {
+        hipLaunchKernelGGL(pack_kn_kernel, dim3(2048), dim3(256), 0, nullptr, staging, w->K, w->N, w->Kp, w->Np,
+                           w->bits, w->W);
+        if (hipGetLastError() != hipSuccess) rc = QLIN_ERR_DEVICE;
+    }
+    if (!rc) rc = upload_scales(w, scales, hipMemcpyHostToDevice, nullptr);
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = QLIN_ERR_DEVICE;
+    (void)hipFree(staging);
+    if (rc) {
+        qlin_weights_free(w);
+        return rc;
+    }
+    *out = w;
+    return QLIN_OK;
+}
+
+static int create_packed(const qlin_weight_config* config, const void* packed, const float* scales,
+                         hipMemcpyKind kind, hipStream_t st, qlin_weights** out) {
+    if (!out) return QLIN_ERR_PARAM;
+    *out = nullptr;
+    if (int rc = check_config(config)) return rc;
+    if (!packed || !scales) return QLIN_ERR_PARAM;
+    if (config->bits == 4 && (config->K & 1)) return QLIN_ERR_PARAM;
+    if (kind == hipMemcpyHostToDevice) {
+        if (int rc = check_scales(scales, config->N)) return rc;
+        if (config->bits == 8) {
+            const int8_t* c = static_cast<const int8_t*>(packed);
+            for (int64_t i = 0; i < (int64_t)config->K * config->N; ++i)
+                if (c[i] == -128) return QLIN_ERR_PARAM;
+        }
+    }
+    qlin_weights* w = nullptr;
+    if (int rc = alloc_weights(config, &w)) return rc;
+    const size_t src_row = config->bits == 4 ? (size_t)config->K / 2 : (size_t)config->K;
+    int rc = QLIN_OK;
+    if (hipMemsetAsync(w->W, 0, (size_t)w->Np * w->wrow, st) != hipSuccess ||
+        hipMemcpy2DAsync(w->W, (size_t)w->wrow, packed, src_row, src_row, (size_t)config->N, kind, st) != hipSuccess)
+        rc = QLIN_ERR_DEVICE;
+    if (!rc) rc = upload_scales(w, scales, kind, st);
+    if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = QLIN_ERR_DEVICE;
+    if (rc) {
+        qlin_weights_free(w);
+        return rc;
+    }
+    *out = w;
+    return QLIN_OK;
+}
+
+int qlin_weights_create_packed(const qlin_weight_config* config, const void* packed_nk, const float* scales,
+                               qlin_weights** out) {
+    return create_packed(config, packed_nk, scales, hipMemcpyHostToDevice, nullptr, out);
+}
+
+int qlin_weights_create_packed_device(const qlin_weight_config* config, const void* packed_nk,
+                                      const float* scales, void* stream, qlin_weights** out) {
+    return create_packed(config, packed_nk, scales, hipMemcpyDeviceToDevice, (hipStream_t)stream, out);
+}
+
+void qlin_weights_free(qlin_weights* w) {
+    if (!w) return;
+    (void)hipFree(w->W);
+    (void)hipFree(w->scales);
+    delete w;
+}
+
+int qlin_weights_query(const qlin_weights* w, qlin_weight_info* out) {
+    if (!w || !out) return QLIN_ERR_PARAM;
+    out->bits = w->bits;
+    out->K = w->K;
+    out->N = w->N;
+    out->K_padded = w->Kp;
+    out->N_padded = w->Np;
+    out->device = w->device;
+    out->device_bytes = (uint64_t)w->Np * w->wrow + (uint64_t)w->Np * sizeof(float);
+    return QLIN_OK;
+}
+
+int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_workspace** out) {
+    if (!out) return QLIN_ERR_PARAM;
+    *out = nullptr;
+    if (max_rows <= 0 || max_k <= 0 || max_n <= 0 || max_k > kMaxK || max_n > (1 << 30)) return QLIN_ERR_PARAM;
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    auto* ws = new (std::nothrow) qlin_workspace();
+    if (!ws) return QLIN_ERR_NOMEM;
+    ws->max_rows = max_rows;
+    ws->max_k = max_k;
+    ws->max_n = max_n;
+    ws->max_kp = (int)round_up(max_k, kKAlign);
+    ws->max_np = (int)round_up(max_n, kNAlign);
+    ws->device = dev;
+    ws->cu_count = cu_count(dev);
+    ws->n_counters = std::max(ws->max_np / 16, 8192);
+    const size_t bq = (size_t)max_rows * ws->max_kp, bs = (size_t)max_rows * sizeof(float);
+    const size_t bgp = (size_t)kGemvMaxRows * ws->max_np * sizeof(int32_t);
+    const size_t bc = (size_t)ws->n_counters * sizeof(uint32_t);
+    const size_t bgm = (size_t)kGemmPartTiles * 64 * 256 * sizeof(int32_t);
+    const size_t bA = (size_t)max_rows * max_k * sizeof(float), bC = (size_t)max_rows * max_n * sizeof(float);
+    bool ok = hipMalloc(&ws->q, bq) == hipSuccess && hipMalloc(&ws->s, bs) == hipSuccess &&
+              hipMalloc(&ws->gemv_part, bgp) == hipSuccess && hipMalloc(&ws->counters, bc) == hipSuccess &&
+              hipMalloc(&ws->gemm_part, bgm) == hipSuccess && hipMalloc(&ws->err, 256) == hipSuccess &&
+              hipMalloc(&ws->dA, bA) == hipSuccess && hipMalloc(&ws->dC, bC) == hipSuccess &&
+              hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess;
+    if (ok)
+        ok = hipMemset(ws->gemv_part, 0, bgp) == hipSuccess && hipMemset(ws->counters, 0, bc) == hipSuccess &&
+             hipMemset(ws->err, 0, 256) == hipSuccess && hipMemset(ws->q, 0, bq) == hipSuccess &&
+             hipDeviceSynchronize() == hipSuccess;
+    ws->device_bytes = bq + bs + bgp + bc + bgm + 256 + bA + bC;
+    ws->last = ws->stream;
+    if (!ok) {
+        qlin_workspace_free(ws);
+        return QLIN_ERR_NOMEM;
+    }
+    *out = ws;
+    return QLIN_OK;
+}
+
+void qlin_workspace_free(qlin_workspace* ws) {
+    if (!ws) return;
+    if (ws->stream) {
+        (void)hipStreamSynchronize(ws->stream);
+        (void)hipStreamDestroy(ws->stream);
+    }
+    (void)hipFree(ws->q);
+    (void)hipFree(ws->s);
+    (void)hipFree(ws->gemv_part);
+    (void)hipFree(ws->counters);
+    (void)hipFree(ws->gemm_part);
+    (void)hipFree(ws->err);
+    (void)hipFree(ws->dA);
+    (void)hipFree(ws->dC);
+    delete ws;
+}
+
+int qlin_workspace_query(const qlin_workspace* ws, qlin_workspace_info* out) {
+    if (!ws || !out) return QLIN_ERR_PARAM;
+    out->max_rows = ws->max_rows;
+    out->reserved = 0;
+    out->device_bytes = ws->device_bytes;
+    out->pinned_host_bytes = 0;
+    return QLIN_OK;
+}
+
+int qlin_workspace_status(qlin_workspace* ws, int32_t clear) {
+    if (!ws) return QLIN_ERR_PARAM;
+    uint32_t e = 0;
+    if (hipStreamSynchronize(ws->last) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (hipMemcpy(&e, ws->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (clear && e && hipMemset(ws->err, 0, sizeof(uint32_t)) != hipSuccess) return QLIN_ERR_DEVICE;
+    return e ? QLIN_ERR_NONFINITE : QLIN_OK;
+}
+
+int qlin_quantize(int32_t rows, int32_t K, const void* A, int32_t a_dtype, int64_t lda, const float* gamma,
+                  float eps, int8_t* q, int64_t ldq, float* s, uint32_t* err, uint32_t flags, void* stream) {
+    if (rows <= 0 || K <= 0 || !A || !q || !s || lda < K || ldq < K || (a_dtype != QLIN_F32 && a_dtype != QLIN_F16))
+        return QLIN_ERR_PARAM;
+    if (gamma && !(eps > 0.0f && std::isfinite(eps))) return QLIN_ERR_PARAM;
+    QuantParams p{};
+    p.A = A;
+    p.lda = lda;
+    p.a_f16 = a_dtype == QLIN_F16;
+    p.K = K;
+    p.ldq = ldq;
+    p.q = q;
+    p.s = s;
+    p.err = err;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.flags = flags;
+    return launch_quant(p, rows, (hipStream_t)stream) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+}  // extern "C"
+
+namespace {
+
+int choose_gemv_splits(const qlin_workspace* ws, int groups, int total_steps, int M, int bits) {
+    int S = env_int("QLIN_GEMV_SPLITS", 0);
+    if (S <= 0) {
+        const int target = env_int("QLIN_GEMV_TARGET_WGS", 2 * ws->cu_count);
+        S = (target + groups - 1) / groups;
+        S = std::min(S, std::max(1, total_steps / 4));
+    }
+    S = std::max(1, std::min(S, total_steps));
+    // keep the LDS copy of the activation slice within 48 KiB
+    while (S < total_steps &&
+           qlin::gemv_lds_bytes_for(M, (total_steps + S - 1) / S, bits) > 48 * 1024)
+        ++S;
+    return S;
+}
+
+int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
+             const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
+             int64_t ldc, uint32_t flags, hipStream_t st) {
+    const bool sw = (flags & kFlagSwiglu) != 0;
+    GemvParams p{};
+    p.W = w->W;
+    p.wscale = w->scales;
+    p.wrow = w->wrow;
+    p.K = w->K;
+    p.Kp = w->Kp;
+    p.N = w->N;
+    p.Np = w->Np;
+    p.M = rows;
+    p.A = A;
+    p.lda = lda;
+    p.a_f16 = a_f16;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.q = q;
+    p.ldq = ldq;
+    p.s = s;
+    p.C = C;
+    p.ldc = ldc;
+    p.c_kind = c_kind;
+    p.flags = flags;
+    p.part = ws->gemv_part;
+    p.counters = ws->counters;
+    p.err = ws->err;
+    const int KS = w->bits == 4 ? 256 : 128;
+    const int total_steps = w->Kp / KS;
+    const int groups = (sw ? w->N / 2 : w->Np) / 16;
+    int S = choose_gemv_splits(ws, groups, total_steps, rows, w->bits);
+    p.steps_per_split = (total_steps + S - 1) / S;
+    p.splits = (total_steps + p.steps_per_split - 1) / p.steps_per_split;
+    if (qlin::gemv_lds_bytes_for(rows, p.steps_per_split, w->bits) > 64 * 1024) return QLIN_ERR_UNSUPPORTED;
+    if (groups > ws->n_counters) return QLIN_ERR_UNSUPPORTED;
+    return launch_gemv(p, w->bits, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* q, int64_t ldq, const float* s,
+             void* C, int c_kind, int64_t ldc, uint32_t flags, hipStream_t st) {
+    const bool sw = (flags & kFlagSwiglu) != 0;
+    GemmParams p{};
+    p.W = w->W;
+    p.wscale = w->scales;
+    p.wrow = w->wrow;
+    p.K = w->K;
+    p.Kp = w->Kp;
+    p.N = w->N;
+    p.Np = w->Np;
+    p.M = rows;
+    p.q = q;
+    p.ldq = ldq;
+    p.s = s;
+    p.C = C;
+    p.ldc = ldc;
+    p.c_kind = c_kind;
+    p.flags = flags;
+    p.m_tiles = (rows + kGemmTile - 1) / kGemmTile;
+    p.n_tiles = sw ? (w->N / 2 + 63) / 64 : (w->N + kGemmTile - 1) / kGemmTile;
+    const int ktiles = w->Kp / kGemmTile;
+    const int tiles = p.m_tiles * p.n_tiles;
+    int S = env_int("QLIN_GEMM_SPLITS", 0);
+    if (S <= 0) {
+        const int target = env_int("QLIN_GEMM_TARGET_WGS", ws->cu_count);
+        S = (target + tiles / 2) / tiles;
+        S = std::min(S, std::max(1, ktiles / 4));
+    }
+    S = std::max(1, std::min(S, ktiles));
+    while (S > 1 && (tiles * S > kGemmPartTiles || tiles > ws->n_counters)) --S;
+    p.ktiles_per_split = (ktiles + S - 1) / S;
+    p.splits = (ktiles + p.ktiles_per_split - 1) / p.ktiles_per_split;
+    p.part = ws->gemm_part;
+    p.counters = ws->counters;
+    return launch_gemm(p, w->bits, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+int check_run(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags) {
+    if (!ws || !w || rows <= 0 || rows > ws->max_rows) return QLIN_ERR_PARAM;
+    if (w->Kp > ws->max_kp || w->Np > ws->max_np) return QLIN_ERR_PARAM;
+    if (w->device != ws->device) return QLIN_ERR_PARAM;
+    if ((flags & kFlagSwiglu) && (w->N % 64 != 0)) return QLIN_ERR_UNSUPPORTED;
+    return QLIN_OK;
+}
+
+int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_dtype, int64_t lda,
+             const float* gamma, float eps, void* C, int c_dtype, int64_t ldc, uint32_t flags, hipStream_t st) {
+    if (int rc = check_run(ws, w, rows, flags)) return rc;
+    if (!A || !C || lda < w->K || (a_dtype != QLIN_F32 && a_dtype != QLIN_F16) ||
+        (c_dtype != QLIN_F32 && c_dtype != QLIN_F16))
+        return QLIN_ERR_PARAM;
+    const int ncols = (flags & kFlagSwiglu) ? w->N / 2 : w->N;
+    if (ldc < ncols) return QLIN_ERR_PARAM;
+    if (gamma && !(eps > 0.0f && std::isfinite(eps))) return QLIN_ERR_PARAM;
+    ws->last = st;
+    const int fused_max = env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4);
+    if (gemv_ok(ws, w, rows) && !(flags & kFlagNoFusedQuant) && rows <= fused_max) {
+        return run_gemv(ws, w, rows, A, a_dtype == QLIN_F16, lda, gamma, eps, nullptr, 0, nullptr, C,
+                        c_dtype == QLIN_F16, ldc, flags, st);
+    }
+    QuantParams qp{};
+    qp.A = A;
+    qp.lda = lda;
+    qp.a_f16 = a_dtype == QLIN_F16;
+    qp.K = w->K;
+    qp.ldq = w->Kp;
+    qp.q = ws->q;
+    qp.s = ws->s;
+    qp.err = ws->err;
+    qp.gamma = gamma;
+    qp.eps = eps;
+    qp.flags = flags;
+    if (launch_quant(qp, rows, st) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (gemv_ok(ws, w, rows))
+        return run_gemv(ws, w, rows, nullptr, 0, 0, nullptr, 0.0f, ws->q, w->Kp, ws->s, C, c_dtype == QLIN_F16,
+                        ldc, flags, st);
+    return run_gemm(ws, w, rows, ws->q, w->Kp, ws->s, C, c_dtype == QLIN_F16 ? 1 : 0, ldc, flags, st);
+}
+
+int run_host(qlin_workspace* ws, const qlin_weights* w, int rows, const float* A, float* C, uint32_t flags) {
+    if (int rc = check_run(ws, w, rows, flags)) return rc;
+    if (!A || !C) return QLIN_ERR_PARAM;
+    if (w->K > ws->max_k || w->N > ws->max_n) return QLIN_ERR_PARAM;
+    const int ncols = (flags & kFlagSwiglu) ? w->N / 2 : w->N;
+    hipStream_t st = ws->stream;
+    if (hipMemsetAsync(ws->err, 0, sizeof(uint32_t), st) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (hipMemcpyAsync(ws->dA, A, (size_t)rows * w->K * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess)
+        return QLIN_ERR_DEVICE;
+    if (int rc = run_impl(ws, w, rows, ws->dA, QLIN_F32, w->K, nullptr, 0.0f, ws->dC, QLIN_F32, ncols, flags, st))
+        return rc;
+    if (hipMemcpyAsync(C, ws->dC, (size_t)rows * ncols * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess)
+        return QLIN_ERR_DEVICE;
+    uint32_t e = 0;
+    if (hipMemcpyAsync(&e, ws->err, sizeof(e), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return QLIN_ERR_DEVICE;
+    return e ? QLIN_ERR_NONFINITE : QLIN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qlin_run_f32(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const float* A, float* C) {
+    return run_host(ws, w, rows, A, C, 0);
+}
+
+int qlin_run_swiglu_f32(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const float* A, float* C) {
+    return run_host(ws, w, rows, A, C, kFlagSwiglu);
+}
+
+int qlin_run(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const void* A, int32_t a_dtype,
+             int64_t lda, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream) {
+    return run_impl(ws, w, rows, A, a_dtype, lda, nullptr, 0.0f, C, c_dtype, ldc, flags, (hipStream_t)stream);
+}
+
+int qlin_run_rmsnorm(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const void* A, int32_t a_dtype,
+                     int64_t lda, const float* gamma, float eps, void* C, int32_t c_dtype, int64_t ldc,
+                     uint32_t flags, void* stream) {
+    if (!gamma) return QLIN_ERR_PARAM;
+    return run_impl(ws, w, rows, A, a_dtype, lda, gamma, eps, C, c_dtype, ldc, flags, (hipStream_t)stream);
+}
+
+int qlin_gemm_i32(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const int8_t* q, int64_t ldq,
+                  int32_t* acc, int64_t ldacc, void* stream) {
+    if (int rc = check_run(ws, w, rows, 0)) return rc;
+    if (!q || !acc || ldq < w->Kp || ldq % 16 || (reinterpret_cast<uintptr_t>(q) & 15) || ldacc < w->N)
+        return QLIN_ERR_PARAM;
+    ws->last = (hipStream_t)stream;
+    if (gemv_ok(ws, w, rows))
+        return run_gemv(ws, w, rows, nullptr, 0, 0, nullptr, 0.0f, q, ldq, nullptr, acc, 2, ldacc, 0,
+                        (hipStream_t)stream);
+    return run_gemm(ws, w, rows, q, ldq, nullptr, acc, 2, ldacc, 0, (hipStream_t)stream);
+}
+
+int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const int8_t* q, int64_t ldq,
+                       const float* s, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream) {
+    if (int rc = check_run(ws, w, rows, flags)) return rc;
+    const int ncols = (flags & kFlagSwiglu) ? w->N / 2 : w->N;
+    if (!q || !s || !C || ldq < w->Kp || ldq % 16 || (reinterpret_cast<uintptr_t>(q) & 15) || ldc < ncols ||
+        (c_dtype != QLIN_F32 && c_dtype != QLIN_F16))
+        return QLIN_ERR_PARAM;
+    hipStream_t st = (hipStream_t)stream;
+    ws->last = st;
+    if (gemv_ok(ws, w, rows))
+        return run_gemv(ws, w, rows, nullptr, 0, 0, nullptr, 0.0f, q, ldq, s, C, c_dtype == QLIN_F16, ldc,
+                        flags, st);
+    return run_gemm(ws, w, rows, q, ldq, s, C, c_dtype == QLIN_F16 ? 1 : 0, ldc, flags, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,149 @@
+// Internal declarations shared by the HIP translation units of libqlinear.
+//
+// Device layout of the weights (see qlin_capi.hip for the repack):
+//   W4: [Np, Kp/2] bytes, byte j of row n holds k = 2j (low nibble) and 2j+1 (high
+//       nibble) as two's-complement 4-bit codes;
+//   W8: [Np, Kp] int8;
+//   scales: f32 [Np], zero in the padded rows.
+// Kp = roundup(K, 256), Np = roundup(N, 64); pad codes are zero so they add nothing.
+//
+// Quantized activations: int8 [M, ldq] with ldq >= Kp and zeros in [K, Kp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+constexpr int kKAlign = 256;  // Kp alignment (one GEMV wave step of W4 spans 256 k)
+constexpr int kNAlign = 64;   // Np alignment
+constexpr int kMaxK = 131072; // int32 accumulators cannot overflow below this K (W4 codes x16)
+constexpr int kGemvMaxRows = 16;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+enum : uint32_t {
+    kFlagRne = 0x1u,
+    kFlagNormSeq = 0x2u,
+    kFlagSwiglu = 0x4u,
+    kFlagNoFusedQuant = 0x8u,
+};
+
+struct QuantParams {
+    const void* A;
+    int64_t lda;
+    int a_f16;
+    int K;
+    int64_t ldq;     // q row stride; columns [K, ldq) are zero-filled
+    int8_t* q;
+    float* s;
+    uint32_t* err;   // bit 0 set on non-finite input (may be null)
+    const float* gamma;  // RMSNorm weight, null = no norm
+    float eps;
+    uint32_t flags;
+};
+
+struct GemvParams {
+    const uint8_t* W;     // device layout
+    const float* wscale;  // [Np]
+    int64_t wrow;         // bytes per weight row
+    int K, Kp, N, Np, M;
+    // activations: either raw rows quantized in the prologue (A != null) ...
+    const void* A;
+    int64_t lda;
+    int a_f16;
+    const float* gamma;
+    float eps;
+    // ... or rows already quantized
+    const int8_t* q;
+    int64_t ldq;
+    const float* s;
+    void* C;
+    int64_t ldc;
+    int c_kind;         // 0 f32, 1 f16, 2 int32 acc (stage entry point)
+    uint32_t flags;
+    int splits;         // workgroups per row group along K
+    int steps_per_split;
+    int32_t* part;      // [kGemvMaxRows, Np] int32, zero at rest
+    uint32_t* counters; // [Np/16], zero at rest
+    uint32_t* err;
+};
+
+struct GemmParams {
+    const uint8_t* W;
+    const float* wscale;
+    int64_t wrow;
+    int K, Kp, N, Np, M;
+    const int8_t* q;
+    int64_t ldq;
+    const float* s;       // null: write raw int32 acc (stage entry point)
+    void* C;
+    int64_t ldc;
+    int c_kind;           // 0 f32, 1 f16, 2 int32 acc
+    uint32_t flags;
+    int m_tiles, n_tiles, splits, ktiles_per_split;
+    int32_t* part;        // split-K partials, tile-major
+    uint32_t* counters;   // [m_tiles * n_tiles], zero at rest
+};
+
+// Launchers (return hipError_t of the launch).
+hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream);
+hipError_t launch_gemv(const GemvParams& p, int bits, hipStream_t stream);
+hipError_t launch_gemm(const GemmParams& p, int bits, hipStream_t stream);
+hipError_t launch_pack_w4(const int8_t* codes_nk, int N, int K, int Np, int Kp, uint8_t* out,
+                          hipStream_t stream);
+
+// ---- device helpers -------------------------------------------------------
+
+__device__ __forceinline__ float qscale_from_absmax(float absmax) {
+    // src/npu.rs:1102-1105
+    if (absmax == 0.0f) return 1.0f;
+    float s = absmax / 127.0f;  // IEEE division (correctly rounded build flag)
+    return s < 1.17549435e-38f ? 1.17549435e-38f : s;
+}
+
+__device__ __forceinline__ int quant_one(float x, float inv, bool rne) {
+    // src/npu.rs:1109: (x * (1.0 / scale)).round().clamp(-127.0, 127.0) as i32
+    float v = x * inv;
+    float r = rne ? __builtin_rintf(v) : __builtin_roundf(v);
+    if (r != r) return 0;  // NaN -> 0, Rust's saturating cast
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+// fp16 store of an f32 result, rounded twice as specified (to f32 by the producing
+// operation, then to fp16 to nearest even).  The empty asm pins x in a VGPR as a
+// rounded f32 value; without it the backend folds the producing multiply into
+// v_fma_mixlo_f16, which rounds the exact product once, straight to fp16.
+__device__ __forceinline__ _Float16 f16_of_f32(float x) {
+    __asm__ volatile("" : "+v"(x));
+    return (_Float16)x;
+}
+
+// Waits until every memory operation this wave issued has completed (vmcnt,
+// expcnt and lgkmcnt all zero).  Used before a workgroup barrier that precedes a
+// split-K counter bump: partials are written with device-coherent (sc1) stores or
+// L2 atomics, so completion is all the ordering needed, and the L2 writeback +
+// invalidate of an agent-scope fence is avoided.
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ void store_coherent(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t load_coherent(const int32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace qlin

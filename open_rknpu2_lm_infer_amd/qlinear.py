@@ -1,0 +1,166 @@
+"""Device-tensor front end of the C ABI (include/qlinear.h) for torch callers.
+
+torch supplies device memory and streams; every computation is a libqlinear.so
+kernel launched on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import (QLIN_F16, QLIN_F32, QLIN_NO_FUSED_QUANT, QLIN_NORM_SEQUENTIAL,  # noqa: F401
+                   QLIN_ROUND_HALF_EVEN, QLIN_SWIGLU, check)
+
+_DT = {torch.float32: QLIN_F32, torch.float16: QLIN_F16}
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Weights:
+    """Device-resident W4/W8 codes + per-channel scales (qlin_weights)."""
+
+    def __init__(self, handle: ctypes.c_void_p):
+        self.handle = handle
+        info = _lib.WeightInfo()
+        check(_lib.load().qlin_weights_query(handle, ctypes.byref(info)), "qlin_weights_query")
+        self.bits, self.K, self.N = info.bits, info.K, info.N
+        self.K_padded, self.N_padded = info.K_padded, info.N_padded
+        self.device_bytes = info.device_bytes
+
+    @classmethod
+    def from_codes_kn(cls, bits: int, codes_kn: np.ndarray, scales: np.ndarray) -> "Weights":
+        """Reference QuantMatrix layout: int8 [K, N] K-major + f32 [N]."""
+        codes_kn = np.ascontiguousarray(codes_kn, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        K, N = codes_kn.shape
+        cfg = _lib.WeightConfig(bits, K, N)
+        h = ctypes.c_void_p()
+        check(_lib.load().qlin_weights_create(ctypes.byref(cfg), codes_kn.ctypes.data_as(ctypes.c_void_p),
+                                              scales.ctypes.data_as(ctypes.c_void_p), ctypes.byref(h)),
+              "qlin_weights_create")
+        return cls(h)
+
+    @classmethod
+    def from_packed_device(cls, bits: int, K: int, N: int, packed: torch.Tensor,
+                           scales: torch.Tensor) -> "Weights":
+        """Device layout on the GPU: uint8 [N, K/2] (W4) or int8 [N, K] (W8) + f32 [N]."""
+        assert packed.is_cuda and scales.is_cuda and packed.is_contiguous() and scales.is_contiguous()
+        cfg = _lib.WeightConfig(bits, K, N)
+        h = ctypes.c_void_p()
+        check(_lib.load().qlin_weights_create_packed_device(ctypes.byref(cfg), _ptr(packed), _ptr(scales),
+                                                            _stream(), ctypes.byref(h)),
+              "qlin_weights_create_packed_device")
+        return cls(h)
+
+    def close(self):
+        if self.handle:
+            _lib.load().qlin_weights_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Workspace:
+    """Scratch for runs of up to max_rows rows over weights up to max_k x max_n."""
+
+    def __init__(self, max_rows: int, max_k: int, max_n: int):
+        self.handle = ctypes.c_void_p()
+        check(_lib.load().qlin_workspace_create(max_rows, max_k, max_n, ctypes.byref(self.handle)),
+              "qlin_workspace_create")
+        self.max_rows = max_rows
+
+    def status(self, clear: bool = True) -> int:
+        return _lib.load().qlin_workspace_status(self.handle, int(clear))
+
+    def close(self):
+        if self.handle:
+            _lib.load().qlin_workspace_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def run(ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor | None = None,
+        out_dtype=torch.float16, flags: int = 0, gamma: torch.Tensor | None = None,
+        eps: float = 1e-6) -> torch.Tensor:
+    """out[M, N] (or [M, N/2] with QLIN_SWIGLU) = quantized linear of A[M, K] (device)."""
+    M = A.shape[0]
+    ncols = w.N // 2 if flags & QLIN_SWIGLU else w.N
+    if out is None:
+        out = torch.empty((M, ncols), dtype=out_dtype, device=A.device)
+    assert A.stride(1) == 1 and out.stride(1) == 1
+    L = _lib.load()
+    if gamma is None:
+        rc = L.qlin_run(ws.handle, w.handle, M, _ptr(A), _DT[A.dtype], A.stride(0), _ptr(out), _DT[out.dtype],
+                        out.stride(0), flags, _stream())
+    else:
+        rc = L.qlin_run_rmsnorm(ws.handle, w.handle, M, _ptr(A), _DT[A.dtype], A.stride(0), _ptr(gamma), eps,
+                                _ptr(out), _DT[out.dtype], out.stride(0), flags, _stream())
+    check(rc, "qlin_run")
+    return out
+
+
+def quantize(A: torch.Tensor, ldq: int | None = None, gamma: torch.Tensor | None = None, eps: float = 1e-6,
+             flags: int = 0, err: torch.Tensor | None = None):
+    """Per-token quantization alone: returns (q int8 [M, ldq], s f32 [M])."""
+    M, K = A.shape
+    ldq = ldq or K
+    q = torch.empty((M, ldq), dtype=torch.int8, device=A.device)
+    s = torch.empty((M,), dtype=torch.float32, device=A.device)
+    check(_lib.load().qlin_quantize(M, K, _ptr(A), _DT[A.dtype], A.stride(0),
+                                    _ptr(gamma) if gamma is not None else None, eps, _ptr(q), ldq, _ptr(s),
+                                    _ptr(err) if err is not None else None, flags, _stream()),
+          "qlin_quantize")
+    return q, s
+
+
+def gemm_i32(ws: Workspace, w: Weights, q: torch.Tensor) -> torch.Tensor:
+    M = q.shape[0]
+    acc = torch.empty((M, w.N), dtype=torch.int32, device=q.device)
+    check(_lib.load().qlin_gemm_i32(ws.handle, w.handle, M, _ptr(q), q.stride(0), _ptr(acc), acc.stride(0),
+                                    _stream()), "qlin_gemm_i32")
+    return acc
+
+
+def run_quantized(ws: Workspace, w: Weights, q: torch.Tensor, s: torch.Tensor, out_dtype=torch.float16,
+                  flags: int = 0) -> torch.Tensor:
+    M = q.shape[0]
+    ncols = w.N // 2 if flags & QLIN_SWIGLU else w.N
+    out = torch.empty((M, ncols), dtype=out_dtype, device=q.device)
+    check(_lib.load().qlin_run_quantized(ws.handle, w.handle, M, _ptr(q), q.stride(0), _ptr(s), _ptr(out),
+                                         _DT[out_dtype], out.stride(0), flags, _stream()), "qlin_run_quantized")
+    return out
+
+
+def run_host_f32(ws: Workspace, w: Weights, A: np.ndarray, swiglu: bool = False) -> np.ndarray:
+    """The synchronous host-buffer entry (drop-in for rk_npu_w4a8_run_f32 / _run_swiglu_f32)."""
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    M = A.shape[0]
+    out = np.zeros((M, w.N // 2 if swiglu else w.N), np.float32)
+    fn = _lib.load().qlin_run_swiglu_f32 if swiglu else _lib.load().qlin_run_f32
+    rc = fn(ws.handle, w.handle, M, A.ctypes.data_as(ctypes.c_void_p), out.ctypes.data_as(ctypes.c_void_p))
+    check(rc, "qlin_run_f32")
+    return out
+
+
+def pack_w4_nk(codes_nk: np.ndarray) -> np.ndarray:
+    """[N, K] codes in [-8, 7] -> [N, K/2] bytes, low nibble = even k (the device layout)."""
+    c = np.ascontiguousarray(codes_nk, dtype=np.int8).astype(np.uint8) & 0xF
+    return (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
