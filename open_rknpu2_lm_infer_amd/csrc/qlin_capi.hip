@@ -13,10 +13,6 @@
 #include "../../include/qlinear.h"
 #include "qlin_internal.hpp"
 
-namespace qlin {
-size_t gemv_lds_bytes_for(int M, int steps_per_split, int bits);
-}
-
 using namespace qlin;
 
 struct qlin_weights {
@@ -356,21 +352,6 @@ int qlin_quantize(int32_t rows, int32_t K, const void* A, int32_t a_dtype, int64
 
 namespace {
 
-int choose_gemv_splits(const qlin_workspace* ws, int groups, int total_steps, int M, int bits) {
-    int S = env_int("QLIN_GEMV_SPLITS", 0);
-    if (S <= 0) {
-        const int target = env_int("QLIN_GEMV_TARGET_WGS", 2 * ws->cu_count);
-        S = (target + groups - 1) / groups;
-        S = std::min(S, std::max(1, total_steps / 4));
-    }
-    S = std::max(1, std::min(S, total_steps));
-    // keep the LDS copy of the activation slice within 48 KiB
-    while (S < total_steps &&
-           qlin::gemv_lds_bytes_for(M, (total_steps + S - 1) / S, bits) > 48 * 1024)
-        ++S;
-    return S;
-}
-
 int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
              const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
              int64_t ldc, uint32_t flags, hipStream_t st) {
@@ -396,18 +377,25 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     p.ldc = ldc;
     p.c_kind = c_kind;
     p.flags = flags;
-    p.part = ws->gemv_part;
-    p.counters = ws->counters;
     p.err = ws->err;
-    const int KS = w->bits == 4 ? 256 : 128;
-    const int total_steps = w->Kp / KS;
+    const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
     const int groups = (sw ? w->N / 2 : w->Np) / 16;
-    int S = choose_gemv_splits(ws, groups, total_steps, rows, w->bits);
-    p.steps_per_split = (total_steps + S - 1) / S;
-    p.splits = (total_steps + p.steps_per_split - 1) / p.steps_per_split;
-    if (qlin::gemv_lds_bytes_for(rows, p.steps_per_split, w->bits) > 64 * 1024) return QLIN_ERR_UNSUPPORTED;
-    if (groups > ws->n_counters) return QLIN_ERR_UNSUPPORTED;
-    return launch_gemv(p, w->bits, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+    int waves = env_int("QLIN_GEMV_WAVES", 0);
+    if (waves != 4 && waves != 8 && waves != 16) waves = gemv_pick_waves(groups, steps);
+    return launch_gemv(p, w->bits, waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+// Whether the decode GEMV may quantize (and normalize) the raw rows itself.
+bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, const float* gamma, uint32_t flags) {
+    if (rows > kGemvMaxRows || (flags & kFlagNoFusedQuant) || rows > env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4))
+        return false;
+    if ((reinterpret_cast<uintptr_t>(A) & 15) || (lda % 8) || (gamma && (reinterpret_cast<uintptr_t>(gamma) & 15)))
+        return false;
+    const bool sw = (flags & kFlagSwiglu) != 0;
+    const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
+    const int waves = gemv_pick_waves((sw ? w->N / 2 : w->Np) / 16, steps);
+    return gemv_can_fuse(rows, w->K, waves, gamma != nullptr) &&
+           (env_int("QLIN_GEMV_WAVES", 0) == 0 || gemv_can_fuse(rows, w->K, env_int("QLIN_GEMV_WAVES", 0), gamma != nullptr));
 }
 
 int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* q, int64_t ldq, const float* s,
@@ -466,8 +454,7 @@ int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     if (ldc < ncols) return QLIN_ERR_PARAM;
     if (gamma && !(eps > 0.0f && std::isfinite(eps))) return QLIN_ERR_PARAM;
     ws->last = st;
-    const int fused_max = env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4);
-    if (gemv_ok(ws, w, rows) && !(flags & kFlagNoFusedQuant) && rows <= fused_max) {
+    if (gemv_fusable(w, rows, A, lda, gamma, flags)) {
         return run_gemv(ws, w, rows, A, a_dtype == QLIN_F16, lda, gamma, eps, nullptr, 0, nullptr, C,
                         c_dtype == QLIN_F16, ldc, flags, st);
     }

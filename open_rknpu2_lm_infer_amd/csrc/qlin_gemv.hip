@@ -3,10 +3,11 @@
 // Replaces the native library's per-call scan/quantize, NPU int4 GEMM and CPU
 // reduce/dequant for small M (QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:24-31).
 //
-// Mapping.  A workgroup (4 waves) owns one group of 16 output channels (plus the
-// matching 16 "up" channels for SwiGLU) and one K slice; `splits` workgroups share
-// a group along K and combine int32 partials with atomics, the last one to arrive
-// running the epilogue and re-zeroing the partials and its counter.
+// Mapping.  One workgroup of WAVES waves owns a group of 16 output channels (plus the
+// matching 16 "up" channels N/2 + j for SwiGLU) over the whole K; wave w takes wave
+// steps w, w + WAVES, ...  Partial sums meet once, in LDS, at the end: no split-K,
+// no atomics, no counters.  WAVES (4, 8 or 16) is picked per shape so that even
+// N = 2560 puts a few thousand waves in flight.
 //
 // Streaming.  One wave step covers 16 weight rows x 128 bytes (a full 128-byte line
 // per row): lane l loads 16 bytes of row l%16 at byte 16*(l/16) and 64 + 16*(l/16).
@@ -14,44 +15,57 @@
 // each 16 bytes unpack in registers into two B operands.  The unpack keeps the
 // nibble in the high half of each byte (w & 0xF0, w << 4 & 0xF0), i.e. 16*code as
 // an exact int8, so the int32 sum is 16x the true one and is shifted back (exact)
-// before dequant.  The two nibble halves come out as even-k / odd-k byte groups;
-// the activation bytes are stored in LDS in that same order so the k index of A
-// and B agree lane by lane.  Rows beyond M feed zeros to the matrix core.
+// before dequant.  The two nibble halves come out as even-k / odd-k byte groups,
+// and the activation bytes are put in that same order (in LDS, or by v_perm_b32
+// after a direct load) so the k index of A and B agree lane by lane.  Rows beyond
+// M feed zeros to the matrix core.
 //
-// Activations.  The prologue quantizes (or copies) the rows for the workgroup's K
-// slice into LDS.  In fused mode every workgroup scans the whole row for its absmax
-// (and RMSNorm sum when gamma is given); max is order independent, so each
-// workgroup derives the same s and q bit for bit.  The first batch of weight loads
-// is issued before the prologue so the scan overlaps HBM latency.
+// Ordering.  Memory counters retire in issue order, so every activation load is
+// issued before the first weight load; waiting for the activations then never
+// waits for the weight stream, which is consumed only after the prologue.
+//
+// Activations.  FUSED (M <= 4): every workgroup loads the raw rows into registers,
+// derives the per-token scale (and the RMSNorm scale) itself and quantizes into LDS;
+// max is order independent, so every workgroup gets the same s and q bit for bit.
+// Otherwise q and s come from the quantize kernel and each lane loads its A operand
+// straight from L2.
+#include <type_traits>
+
 #include "qlin_rows.hpp"
 
 namespace qlin {
 
-constexpr int kGemvThreads = 256;
-constexpr int kGemvBatch = 4;  // wave steps in flight per buffer
+constexpr int kFusedMaxRows = 4;
 
-template <int BITS, bool SWIGLU>
-struct GemvTraits {
-    static constexpr int KS = BITS == 4 ? 256 : 128;  // k per wave step
+// Register budget per wave count (1024-thread workgroups get 128 VGPRs per lane):
+// wave steps in flight per register buffer, and 8-element activation groups held
+// per thread by the fused prologue.
+template <int WAVES, bool FUSED>
+struct GemvCfg {
+    static constexpr int BATCH = FUSED ? (WAVES >= 8 ? 2 : 4) : (WAVES >= 16 ? 1 : 2);
+    static constexpr int XREGS = WAVES >= 16 ? 2 : 8;
 };
+constexpr int fused_regs(int waves) { return waves >= 16 ? 2 : 8; }
 
-__device__ __forceinline__ v4i ld16(const uint8_t* p) {
+__device__ __forceinline__ v4i ld16(const void* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
 
-__device__ __forceinline__ v4i lds16(const uint8_t* p) {
-    return *reinterpret_cast<const v4i*>(p);
+// even-k then odd-k byte order inside each 8-byte group (matches the W4 unpack)
+__device__ __forceinline__ v4i perm_evens_odds(v4i x) {
+    v4i r;
+    r[0] = (int)__builtin_amdgcn_perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u);  // k0 k2 k4 k6
+    r[1] = (int)__builtin_amdgcn_perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u);  // k1 k3 k5 k7
+    r[2] = (int)__builtin_amdgcn_perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u);
+    r[3] = (int)__builtin_amdgcn_perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u);
+    return r;
 }
 
 template <int BITS>
-__device__ __forceinline__ void step_mfma(v4i& acc, const v4i b[2], const uint8_t* arow, bool live) {
-    const v4i zero = {0, 0, 0, 0};
+__device__ __forceinline__ void mfma_step(v4i& acc, const v4i b[2], const v4i a[4]) {
     if constexpr (BITS == 8) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            v4i a = live ? lds16(arow + 64 * j) : zero;
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc, 0, 0, 0);
-        }
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b[1], acc, 0, 0, 0);
     } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -61,277 +75,468 @@ __device__ __forceinline__ void step_mfma(v4i& acc, const v4i b[2], const uint8_
                 lo[d] = (b[j][d] << 4) & 0xF0F0F0F0;
                 hi[d] = b[j][d] & 0xF0F0F0F0;
             }
-            v4i b0 = {lo[0], hi[0], lo[1], hi[1]};
-            v4i b1 = {lo[2], hi[2], lo[3], hi[3]};
-            v4i a0 = live ? lds16(arow + 128 * j) : zero;
-            v4i a1 = live ? lds16(arow + 128 * j + 16) : zero;
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+            const v4i b0 = {lo[0], hi[0], lo[1], hi[1]};
+            const v4i b1 = {lo[2], hi[2], lo[3], hi[3]};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[2 * j], b0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[2 * j + 1], b1, acc, 0, 0, 0);
         }
     }
 }
 
-// Packs 8 quantized values for LDS: natural order for W8, even-k then odd-k for W4.
+// A operand of one wave step: W8 uses a[0..1] (k 64j + 16g), W4 a[0..3] (k 128j + 32g + 16h).
 template <int BITS>
-__device__ __forceinline__ uint2 pack_q8(const int v[8]) {
-    uint32_t w0 = 0, w1 = 0;
+__device__ __forceinline__ void a_from_lds(v4i a[4], const uint8_t* arow) {
     if constexpr (BITS == 8) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w0 |= (uint32_t)(v[i] & 0xff) << (8 * i);
-            w1 |= (uint32_t)(v[4 + i] & 0xff) << (8 * i);
-        }
+        a[0] = ld16(arow);
+        a[1] = ld16(arow + 64);
+    } else {
+        a[0] = ld16(arow);
+        a[1] = ld16(arow + 16);
+        a[2] = ld16(arow + 128);
+        a[3] = ld16(arow + 144);
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void a_from_global(v4i a[4], const int8_t* qrow, bool live) {
+    const v4i zero = {0, 0, 0, 0};
+    if constexpr (BITS == 8) {
+        a[0] = live ? ld16(qrow) : zero;
+        a[1] = live ? ld16(qrow + 64) : zero;
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w0 |= (uint32_t)(v[2 * i] & 0xff) << (8 * i);
-            w1 |= (uint32_t)(v[2 * i + 1] & 0xff) << (8 * i);
+        for (int j = 0; j < 2; ++j) {
+            a[2 * j] = perm_evens_odds(live ? ld16(qrow + 128 * j) : zero);           // k 0..15 of the lane's 32
+            a[2 * j + 1] = perm_evens_odds(live ? ld16(qrow + 128 * j + 16) : zero);  // k 16..31
         }
     }
-    return make_uint2(w0, w1);
 }
 
-template <typename T, int BITS, bool VEC>
-__device__ void stage_fused(const GemvParams& p, uint8_t* lds_a, int stride, int kb, int ke,
-                            float* lds_s, float* lds_red) {
-    const bool gvec = VEC && ((reinterpret_cast<uintptr_t>(p.gamma) & 15) == 0);
-    const bool rne = (p.flags & kFlagRne) != 0;
-    for (int m = 0; m < p.M; ++m) {
-        const T* x = reinterpret_cast<const T*>(p.A) + (int64_t)m * p.lda;
-        float nscale = 1.0f;
-        if (p.gamma) nscale = block_rms_scale<T>(x, p.K, p.eps, (p.flags & kFlagNormSeq) != 0, lds_red);
-        int bad = 0;
-        const float s = block_row_scale<T, VEC>(x, p.K, p.gamma, gvec, nscale, &bad, lds_red);
-        const float inv = 1.0f / s;
-        if (threadIdx.x == 0) {
-            lds_s[m] = s;
-            if (bad && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
-        }
-        for (int k0 = kb + threadIdx.x * 8; k0 < ke; k0 += kGemvThreads * 8) {
-            float v[8];
-            load8<T, VEC>(x, k0, p.K, v);
-            if (p.gamma) {
-                float g[8];
-                load8_gamma(p.gamma, k0, p.K, gvec, g);
-                apply_norm8(v, g, nscale);
-            }
-            int qv[8];
+// Registers of BATCH wave steps: weights (gate, up) and, when the rows arrive
+// quantized, the matching A operands.
+template <int BATCH, bool FUSED>
+struct StepBuf {
+    v4i bg[BATCH][2], bu[BATCH][2];
+    v4i a[FUSED ? 1 : BATCH][4];
+};
+
+// Issues the loads of one batch with no branches: steps past the end re-read the
+// last step (an L2 hit), so the compiler can count outstanding loads exactly and
+// never has to wait for more than it consumes.  In the quantized mode the A loads
+// of a step are issued before its weights.
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH>
+__device__ __forceinline__ void load_batch(StepBuf<BATCH, FUSED>& s, const uint8_t* wg, const uint8_t* wu,
+                                           const int8_t* qrow, bool live, int base, int steps) {
+    constexpr int KS = BITS == 4 ? 256 : 128;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qv[i] = quant_one(v[i], inv, rne);
-            *reinterpret_cast<uint2*>(lds_a + m * stride + (k0 - kb)) = pack_q8<BITS>(qv);
+    for (int i = 0; i < BATCH; ++i) {
+        const int st = min(base + WAVES * i, steps - 1);
+        if constexpr (!FUSED) a_from_global<BITS>(s.a[i], qrow + st * KS, live);
+        s.bg[i][0] = ld16(wg + (int64_t)st * 128);
+        s.bg[i][1] = ld16(wg + (int64_t)st * 128 + 64);
+        if constexpr (SWIGLU) {
+            s.bu[i][0] = ld16(wu + (int64_t)st * 128);
+            s.bu[i][1] = ld16(wu + (int64_t)st * 128 + 64);
         }
     }
 }
 
-template <int BITS>
-__device__ void stage_quantized(const GemvParams& p, uint8_t* lds_a, int stride, int kb, int ke,
-                                float* lds_s) {
-    if (threadIdx.x < p.M) lds_s[threadIdx.x] = p.s ? p.s[threadIdx.x] : 0.0f;
-    for (int m = 0; m < p.M; ++m) {
-        const int8_t* qrow = p.q + (int64_t)m * p.ldq;
-        for (int k0 = kb + threadIdx.x * 8; k0 < ke; k0 += kGemvThreads * 8) {
-            uint2 raw = *reinterpret_cast<const uint2*>(qrow + k0);
-            uint2 out = raw;
-            if constexpr (BITS == 4) {
-                // [k0..k7] -> [k0,k2,k4,k6 | k1,k3,k5,k7]
-                out.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x06040200u);
-                out.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07050301u);
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH>
+__device__ __forceinline__ void compute_batch(v4i& ag, v4i& au, const StepBuf<BATCH, FUSED>& s,
+                                              const uint8_t* arow, int base, int steps) {
+    constexpr int KS = BITS == 4 ? 256 : 128;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        const int st = base + WAVES * i;
+        if (st < steps) {
+            v4i a[4];
+            if constexpr (FUSED) {
+                a_from_lds<BITS>(a, arow + st * KS);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = s.a[i][j];
             }
-            *reinterpret_cast<uint2*>(lds_a + m * stride + (k0 - kb)) = out;
+            mfma_step<BITS>(ag, s.bg[i], a);
+            if constexpr (SWIGLU) mfma_step<BITS>(au, s.bu[i], a);
         }
     }
 }
 
 template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void load_batch(v4i (&bg)[kGemvBatch][2], v4i (&bu)[kGemvBatch][2],
-                                           const uint8_t* wg, const uint8_t* wu, int base, int end) {
-#pragma unroll
-    for (int i = 0; i < kGemvBatch; ++i) {
-        const int st = base + 4 * i;
-        if (st < end) {
-            bg[i][0] = ld16(wg + (int64_t)st * 128);
-            bg[i][1] = ld16(wg + (int64_t)st * 128 + 64);
-            if constexpr (SWIGLU) {
-                bu[i][0] = ld16(wu + (int64_t)st * 128);
-                bu[i][1] = ld16(wu + (int64_t)st * 128 + 64);
-            }
-        }
-    }
-}
-
-template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void compute_batch(v4i& ag, v4i& au, const v4i (&bg)[kGemvBatch][2],
-                                              const v4i (&bu)[kGemvBatch][2], const uint8_t* arow,
-                                              int base, int end, int step_begin, bool live) {
-    constexpr int KS = GemvTraits<BITS, SWIGLU>::KS;
-#pragma unroll
-    for (int i = 0; i < kGemvBatch; ++i) {
-        const int st = base + 4 * i;
-        if (st < end) {
-            const uint8_t* a = arow + (st - step_begin) * KS;
-            step_mfma<BITS>(ag, bg[i], a, live);
-            if constexpr (SWIGLU) step_mfma<BITS>(au, bu[i], a, live);
-        }
-    }
-}
-
-template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void gemv_finish(const GemvParams& p, int m, int n, int r0, int vg,
-                                            int vu, const float* lds_s) {
+__device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, int r0, int vg, int vu, float sm) {
     const int Nh = p.N >> 1;
     const int ag = BITS == 4 ? (vg >> 4) : vg;  // exact: W4 sums carry a factor 16
+    const int cg = r0 + n;
     if (p.c_kind == 2) {
-        if (r0 + n < p.N) reinterpret_cast<int32_t*>(p.C)[(int64_t)m * p.ldc + r0 + n] = ag;
+        if (cg < p.N) reinterpret_cast<int32_t*>(p.C)[(int64_t)m * p.ldc + cg] = ag;
         return;
     }
-    const float sm = lds_s[m];
-    const int cg = r0 + n;
     float out = ((float)ag * sm) * p.wscale[cg];  // src/npu.rs:1117
-    int col = cg;
     if constexpr (SWIGLU) {
         const int au = BITS == 4 ? (vu >> 4) : vu;
         const float up = ((float)au * sm) * p.wscale[Nh + cg];
         out = (out / (1.0f + expf(-out))) * up;  // src/npu.rs:1202-1208
     }
-    const int ncols = SWIGLU ? Nh : p.N;
-    if (col < ncols) {
+    if (cg < (SWIGLU ? Nh : p.N)) {
         if (p.c_kind == 1)
-            reinterpret_cast<_Float16*>(p.C)[(int64_t)m * p.ldc + col] = f16_of_f32(out);
+            reinterpret_cast<_Float16*>(p.C)[(int64_t)m * p.ldc + cg] = f16_of_f32(out);
         else
-            reinterpret_cast<float*>(p.C)[(int64_t)m * p.ldc + col] = out;
+            reinterpret_cast<float*>(p.C)[(int64_t)m * p.ldc + cg] = out;
     }
 }
 
-// MODE 0: q/s given; 1: fused quant of f16 rows; 2: fused quant of f32 rows.
-template <int BITS, bool SWIGLU, int MODE, bool VEC>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvParams p) {
+// Raw activation group of 8 values held in registers until quantization.
+template <typename T>
+struct XGroup;
+template <>
+struct XGroup<__half> {
+    uint4 raw;
+    __device__ __forceinline__ void load(const __half* p) { raw = *reinterpret_cast<const uint4*>(p); }
+    __device__ __forceinline__ void get(float v[8]) const {
+        const __half2* h = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float2 f = __half22float2(h[i]);
+            v[2 * i] = f.x;
+            v[2 * i + 1] = f.y;
+        }
+    }
+};
+template <>
+struct XGroup<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = *reinterpret_cast<const float4*>(p);
+        b = *reinterpret_cast<const float4*>(p + 4);
+    }
+    __device__ __forceinline__ void get(float v[8]) const {
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+};
+
+// Wave-wide max of non-negative floats by DPP (no LDS traffic); valid in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false);
+    return fmaxf(v, __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = dpp_max_step<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_max_step<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_max_step<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_max_step<0x118, 0xf>(v);  // row_shr:8  -> lane 15 of each row holds the row max
+    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// MODE 0: q/s given.  MODE 1: fused quant of fp16 rows.  MODE 2: fused quant of f32 rows.
+// MR: largest row count of the fused modes (1 or 4).  NORM: RMSNorm before the
+// quantization (fused modes, one row).
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
+    using T = typename std::conditional<MODE == 2, float, __half>::type;
+    constexpr bool FUSED = MODE != 0;
+    constexpr int NT = 64 * WAVES;
+    constexpr int KS = BITS == 4 ? 256 : 128;
+    constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
+    constexpr int XR = GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int KS = GemvTraits<BITS, SWIGLU>::KS;
+    __shared__ float s_rows[kGemvMaxRows];
+    __shared__ float s_inv[kFusedMaxRows];
+    __shared__ float s_red[WAVES][kFusedMaxRows];
+    __shared__ int s_bad[WAVES];
+
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rg = blockIdx.x / p.splits, z = blockIdx.x - rg * p.splits;
-    const int total_steps = p.Kp / KS;
-    const int step_begin = z * p.steps_per_split;
-    const int step_end = min(step_begin + p.steps_per_split, total_steps);
-    const int kb = step_begin * KS, ke = step_end * KS;
-    const int stride = p.steps_per_split * KS + 16;
-
-    uint8_t* lds_a = smem;
-    float* lds_s = reinterpret_cast<float*>(smem + p.M * stride);
-    float* lds_red = lds_s + kGemvMaxRows;              // 8 words of reduction scratch
-    int* red = reinterpret_cast<int*>(lds_red + 8);     // [2][4 waves][64 lanes][4]
-    __shared__ int last_flag;
-
-    const int r0 = rg * 16;
+    const int r0 = blockIdx.x * 16;
     const int Nh = p.N >> 1;
-    const uint8_t* wg = p.W + (int64_t)(r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16;
-    const uint8_t* wu = SWIGLU ? p.W + (int64_t)(Nh + r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16
-                               : nullptr;
+    const int steps = p.Kp / KS;
+    const int m_lane = lane & 15;
+    const bool live = m_lane < p.M;
+    const int m_src = min(m_lane, p.M - 1);
 
-    v4i bg0[kGemvBatch][2], bu0[kGemvBatch][2], bg1[kGemvBatch][2], bu1[kGemvBatch][2];
-    int base = step_begin + wave;
-    load_batch<BITS, SWIGLU>(bg0, bu0, wg, wu, base, step_end);
-
-    if constexpr (MODE == 0) {
-        stage_quantized<BITS>(p, lds_a, stride, kb, ke, lds_s);
-    } else if constexpr (MODE == 1) {
-        stage_fused<__half, BITS, VEC>(p, lds_a, stride, kb, ke, lds_s, lds_red);
+    // ---- 1. activation loads (before any weight load) ---------------------------
+    XGroup<T> xr[FUSED ? XR : 1];
+    float gr[NORM ? XR : 1][8];
+    const int ngroups = p.K >> 3;
+    const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
+    const int nreg = FUSED ? p.M * gpt : 0;   // uniform
+    if constexpr (FUSED) {
+        // Only owned groups are loaded.  These loads may sit in branches because every
+        // weight load below is unconditional: waits for them then count exactly the
+        // weight loads issued after them.
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            if (i < nreg) {
+                const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                if (g < ngroups) xr[i].load(reinterpret_cast<const T*>(p.A) + (int64_t)m * p.lda + 8 * g);
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                const int g = tid + NT * i;
+                if (i < gpt && g < ngroups) {
+                    const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
+                    const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
+                    gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
+                    gr[i][4] = b.x; gr[i][5] = b.y; gr[i][6] = b.z; gr[i][7] = b.w;
+                }
+            }
+        }
     } else {
-        stage_fused<float, BITS, VEC>(p, lds_a, stride, kb, ke, lds_s, lds_red);
+        if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
+    }
+
+    // ---- 2. first weight batch ---------------------------------------------------
+    const uint8_t* wg = p.W + (int64_t)(r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16;
+    const uint8_t* wu = SWIGLU ? p.W + (int64_t)(Nh + r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16 : nullptr;
+    const int8_t* qrow = FUSED ? nullptr : p.q + (int64_t)m_src * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16);
+    StepBuf<BATCH, FUSED> b0, b1;
+    int base = wave;
+    load_batch<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, wg, wu, qrow, live, base, steps);
+
+    // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
+    // LDS rows 0..M-1 hold the quantized activations; row M is all zeros and feeds
+    // the matrix-core rows M..15.
+    const int astride = p.Kp + 16;
+    uint8_t* lds_a = smem;
+    if constexpr (FUSED) {
+        const bool rne = (p.flags & kFlagRne) != 0;
+        float nscale = 1.0f;
+        if constexpr (NORM) {
+            // the reference summation order needs the whole row in one place
+            float* lds_x = reinterpret_cast<float*>(smem);
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                const int g = tid + NT * i;
+                if (i < gpt && g < ngroups) {
+                    float v[8];
+                    xr[i].get(v);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) lds_x[8 * g + e] = v[e];
+                }
+            }
+            __syncthreads();
+            if ((p.flags & kFlagNormSeq) != 0) {
+                if (tid == 0) {  // src/ops/norm.rs:38
+                    float sum = 0.0f;
+                    for (int i = 0; i < p.K; ++i) {
+                        const float v2 = lds_x[i] * lds_x[i];
+                        sum = sum + v2;
+                    }
+                    s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+                }
+            } else if (tid < 64) {  // src/model/cpu.rs:14-35, 16 FMA chains
+                const int j = tid & 15;
+                float acc = 0.0f;
+                if (tid < 16)
+                    for (int i = 0; i + 16 <= p.K; i += 16) acc = __builtin_fmaf(lds_x[i + j], lds_x[i + j], acc);
+                const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
+                const float tj = (acc + b) + (c + d);
+                const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
+                if (tid == 0) {
+                    float sum = (tj + t1) + (t2 + t3);
+                    for (int i = p.K & ~15; i < p.K; ++i) {
+                        const float v2 = lds_x[i] * lds_x[i];
+                        sum = sum + v2;
+                    }
+                    s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+                }
+            }
+            __syncthreads();
+            nscale = s_inv[0];
+            __syncthreads();  // lds_x is overwritten by the quantized row below
+        }
+        const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
+        if (owner_wave) {
+            float mx[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+            int bad = 0;
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                if (i < nreg) {
+                    const int m = i / gpt, g = tid + NT * (i - m * gpt);  // m is uniform
+                    if (g < ngroups) {
+                        float v[8];
+                        xr[i].get(v);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
+                        if constexpr (NORM) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                        }
+                        float lm = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
+#pragma unroll
+                        for (int mm = 0; mm < MR; ++mm)
+                            if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < p.M) {
+                    const float w = wave_max_nonneg(mx[m]);
+                    if (lane == 0) s_red[wave][m] = w;
+                }
+            const bool any_bad = __ballot(bad) != 0;
+            if (lane == 0) s_bad[wave] = any_bad;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            const int owners = min(WAVES, (ngroups + 63) / 64);
+            int bad_rows = 0;
+            for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
+            if (bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+            for (int m = 0; m < p.M; ++m) {
+                float am = 0.0f;
+                for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
+                const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+                s_rows[m] = s;
+                s_inv[m] = 1.0f / s;
+            }
+        }
+        __syncthreads();
+        if (owner_wave) {
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                if (i < nreg) {
+                    const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                    if (g < ngroups) {
+                        float v[8];
+                        xr[i].get(v);
+                        if constexpr (NORM) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                        }
+                        const float im = s_inv[m];
+                        int q[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+                        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if constexpr (BITS == 8) {
+                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                            } else {
+                                w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
+                            }
+                        }
+                        *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
+                    }
+                }
+            }
+        }
+        // zero the K..Kp tail of each row and the whole zero row M
+        for (int m = 0; m < p.M; ++m)
+            for (int k = p.K + tid * 8; k < p.Kp; k += NT * 8)
+                *reinterpret_cast<uint2*>(lds_a + m * astride + k) = make_uint2(0, 0);
+        for (int k = tid * 16; k < p.Kp; k += NT * 16)
+            *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
 
-    const int m_lane = lane & 15;
-    const bool live = m_lane < p.M;
-    // rows >= M read row M-1 (in bounds) and feed zeros instead
-    const uint8_t* arow = lds_a + min(m_lane, p.M - 1) * stride + (lane >> 4) * (BITS == 4 ? 32 : 16);
+    // ---- 4. stream the weights through the matrix core ---------------------------
+    const uint8_t* arow = lds_a + (live ? m_lane : p.M) * astride + (lane >> 4) * (BITS == 4 ? 32 : 16);
     v4i ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-    while (base < step_end) {
-        const int nb = base + 4 * kGemvBatch;
-        load_batch<BITS, SWIGLU>(bg1, bu1, wg, wu, nb, step_end);
-        compute_batch<BITS, SWIGLU>(ag, au, bg0, bu0, arow, base, step_end, step_begin, live);
+    while (base < steps) {
+        const int nb = base + WAVES * BATCH;
+        if (nb < steps) load_batch<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, wg, wu, qrow, live, nb, steps);
+        compute_batch<BITS, SWIGLU, FUSED, WAVES, BATCH>(ag, au, b0, arow, base, steps);
         base = nb;
-        if (base >= step_end) break;
-        const int nb2 = base + 4 * kGemvBatch;
-        load_batch<BITS, SWIGLU>(bg0, bu0, wg, wu, nb2, step_end);
-        compute_batch<BITS, SWIGLU>(ag, au, bg1, bu1, arow, base, step_end, step_begin, live);
+        if (base >= steps) break;
+        const int nb2 = base + WAVES * BATCH;
+        if (nb2 < steps) load_batch<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, wg, wu, qrow, live, nb2, steps);
+        compute_batch<BITS, SWIGLU, FUSED, WAVES, BATCH>(ag, au, b1, arow, base, steps);
         base = nb2;
     }
 
-    // cross-wave reduction: lane l holds D[4*(l/16)+i][l%16]
+    // ---- 5. cross-wave reduction and epilogue ------------------------------------
+    // lane l holds D[4*(l/16) + i][l%16]: only lanes < 16*ceil(ROWS/4) carry real rows
+    constexpr int LIVE_LANES = 16 * ((ROWS + 3) / 4);
+    constexpr int REGS = ROWS < 4 ? ROWS : 4;
+    __syncthreads();  // the reduction area reuses the activation area
+    int* red = reinterpret_cast<int*>(smem);  // [2][WAVES][LIVE_LANES][REGS]
+    if (lane < LIVE_LANES) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        red[(wave * 64 + lane) * 4 + i] = ag[i];
-        if constexpr (SWIGLU) red[1024 + (wave * 64 + lane) * 4 + i] = au[i];
-    }
-    __syncthreads();
-    int vg = 0, vu = 0;
-    const int m = tid >> 4, n = tid & 15;
-    const bool owner = tid < 16 * p.M;
-    if (owner) {
-        const int src = (16 * (m >> 2) + n) * 4 + (m & 3);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            vg += red[w * 256 + src];
-            if constexpr (SWIGLU) vu += red[1024 + w * 256 + src];
+        for (int i = 0; i < REGS; ++i) {
+            red[(wave * LIVE_LANES + lane) * REGS + i] = ag[i];
+            if constexpr (SWIGLU) red[WAVES * LIVE_LANES * REGS + (wave * LIVE_LANES + lane) * REGS + i] = au[i];
         }
     }
-    if (p.splits == 1) {
-        if (owner) gemv_finish<BITS, SWIGLU>(p, m, n, r0, vg, vu, lds_s);
-        return;
-    }
-    int32_t* pg = p.part + (int64_t)m * p.Np + r0 + n;
-    int32_t* pu = p.part + (int64_t)m * p.Np + Nh + r0 + n;
-    if (owner) {
-        atomicAdd(pg, vg);  // performed in L2 atomically; device-coherent
-        if constexpr (SWIGLU) atomicAdd(pu, vu);
-    }
-    wait_all_memory();
     __syncthreads();
-    if (tid == 0) last_flag = atomicAdd(&p.counters[rg], 1u) == (unsigned)(p.splits - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    if (owner) {  // atomic exchange reads every split's contribution and re-zeroes the slot
-        vg = atomicExch(pg, 0);
-        if constexpr (SWIGLU) vu = atomicExch(pu, 0);
-        gemv_finish<BITS, SWIGLU>(p, m, n, r0, vg, vu, lds_s);
+    if (tid < 16 * p.M) {
+        const int m = tid >> 4, n = tid & 15;
+        const int src = (16 * (m >> 2) + n) * REGS + (m & 3);
+        int vg = 0, vu = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            vg += red[w * LIVE_LANES * REGS + src];
+            if constexpr (SWIGLU) vu += red[WAVES * LIVE_LANES * REGS + w * LIVE_LANES * REGS + src];
+        }
+        gemv_store<BITS, SWIGLU>(p, m, n, r0, vg, vu, s_rows[m]);
     }
-    if (tid == 0) atomicExch(&p.counters[rg], 0u);
 }
 
-static size_t gemv_lds_bytes(int M, int steps_per_split, int KS) {
-    return (size_t)M * (steps_per_split * KS + 16) + sizeof(float) * (kGemvMaxRows + 8) +
-           sizeof(int) * 2 * 4 * 64 * 4;
+size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm) {
+    size_t a = fused ? (size_t)(M + 1) * (Kp + 16) : 0;
+    if (norm) a = std::max(a, (size_t)M * K * sizeof(float));
+    const size_t red = (size_t)2 * waves * 64 * 4 * sizeof(int);
+    return std::max(a, red);
 }
 
-template <int BITS, bool SWIGLU>
-static hipError_t launch_gemv_t(const GemvParams& p, hipStream_t stream, size_t lds) {
+int gemv_pick_waves(int groups, int steps) {
+    int w = 4;
+    while (w < 16 && groups * w < 3072 && 2 * w <= steps) w *= 2;
+    return w;
+}
+
+bool gemv_can_fuse(int M, int K, int waves, bool norm) {
+    const int nt = 64 * waves;
+    const int gpt = (K / 8 + nt - 1) / nt;
+    if (K % 8 || M > kFusedMaxRows || M * gpt > fused_regs(waves)) return false;
+    if (norm && (M != 1 || (size_t)K * 4 > 64 * 1024)) return false;
+    return true;
+}
+
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR>
+static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
     const int groups = (SWIGLU ? (p.N >> 1) : p.Np) / 16;
-    dim3 grid(groups * p.splits), block(kGemvThreads);
-    const bool vec = p.A && ((reinterpret_cast<uintptr_t>(p.A) & 15) == 0) && (p.lda % 8 == 0) &&
-                     (p.K % 8 == 0);
-    if (!p.A)
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, 0, false>), grid, block, lds, stream, p);
-    else if (p.a_f16 && vec)
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, 1, true>), grid, block, lds, stream, p);
-    else if (p.a_f16)
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, 1, false>), grid, block, lds, stream, p);
-    else if (vec)
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, 2, true>), grid, block, lds, stream, p);
-    else
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, 2, false>), grid, block, lds, stream, p);
+    dim3 grid(groups), block(64 * waves);
+    switch (waves) {
+        case 4: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 4, MR>), grid, block, lds, st, p); break;
+        case 8: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 8, MR>), grid, block, lds, st, p); break;
+        default: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 16, MR>), grid, block, lds, st, p); break;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(const GemvParams& p, int bits, hipStream_t stream) {
-    const int KS = bits == 4 ? 256 : 128;
-    const size_t lds = gemv_lds_bytes(p.M, p.steps_per_split, KS);
-    const bool sw = (p.flags & kFlagSwiglu) != 0;
-    if (bits == 4) return sw ? launch_gemv_t<4, true>(p, stream, lds) : launch_gemv_t<4, false>(p, stream, lds);
-    return sw ? launch_gemv_t<8, true>(p, stream, lds) : launch_gemv_t<8, false>(p, stream, lds);
+template <int BITS, bool SWIGLU, int MODE>
+static hipError_t launch_m(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
+    if (p.gamma) return launch_w<BITS, SWIGLU, MODE, true, 1>(p, waves, lds, st);  // fused norm: one row
+    if (p.M == 1) return launch_w<BITS, SWIGLU, MODE, false, 1>(p, waves, lds, st);
+    return launch_w<BITS, SWIGLU, MODE, false, 4>(p, waves, lds, st);
 }
 
-size_t gemv_lds_bytes_for(int M, int steps_per_split, int bits) {
-    return gemv_lds_bytes(M, steps_per_split, bits == 4 ? 256 : 128);
+template <int BITS, bool SWIGLU>
+static hipError_t launch_b(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
+    if (!p.A) return launch_w<BITS, SWIGLU, 0, false, 1>(p, waves, lds, st);
+    return p.a_f16 ? launch_m<BITS, SWIGLU, 1>(p, waves, lds, st) : launch_m<BITS, SWIGLU, 2>(p, waves, lds, st);
+}
+
+hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream) {
+    const bool fused = p.A != nullptr;
+    const size_t lds = gemv_lds_bytes_for(p.M, p.Kp, p.K, waves, fused, fused && p.gamma != nullptr);
+    const bool sw = (p.flags & kFlagSwiglu) != 0;
+    if (bits == 4) return sw ? launch_b<4, true>(p, waves, lds, stream) : launch_b<4, false>(p, waves, lds, stream);
+    return sw ? launch_b<8, true>(p, waves, lds, stream) : launch_b<8, false>(p, waves, lds, stream);
 }
 
 }  // namespace qlin

@@ -62,11 +62,7 @@ struct GemvParams {
     int64_t ldc;
     int c_kind;         // 0 f32, 1 f16, 2 int32 acc (stage entry point)
     uint32_t flags;
-    int splits;         // workgroups per row group along K
-    int steps_per_split;
-    int32_t* part;      // [kGemvMaxRows, Np] int32, zero at rest
-    uint32_t* counters; // [Np/16], zero at rest
-    uint32_t* err;
+    uint32_t* err;      // bit 0 set on non-finite input (fused quantization)
 };
 
 struct GemmParams {
@@ -88,7 +84,10 @@ struct GemmParams {
 
 // Launchers (return hipError_t of the launch).
 hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream);
-hipError_t launch_gemv(const GemvParams& p, int bits, hipStream_t stream);
+hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream);
+int gemv_pick_waves(int groups, int steps);
+bool gemv_can_fuse(int M, int K, int waves, bool norm);
+size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm);
 hipError_t launch_gemm(const GemmParams& p, int bits, hipStream_t stream);
 hipError_t launch_pack_w4(const int8_t* codes_nk, int N, int K, int Np, int Kp, uint8_t* out,
                           hipStream_t stream);
