@@ -14,6 +14,12 @@ launch stream), int8 TOPS of the M=512 prefill GEMMs of the same layer, and the
 CPU oracle timed on the host cores over a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--prefill-reps R]
+    python bench.py --mode kernel   # only the dominant kernel, for rocprofv3 --pmc passes
+    python bench.py --mode copy     # a plain 256 MiB device copy, the counters' calibration
+
+roofline.traffic is read from profiles/gemv_gate_up_w4_m1_traffic.txt (written by
+open_rknpu2_lm_infer_amd.profsum from FETCH_SIZE / WRITE_SIZE passes over
+`--mode kernel`, scaled by the same counters over `--mode copy`).
 """
 from __future__ import annotations
 
@@ -31,6 +37,18 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel, as measured by rocprofv3 counters."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_gate_up_w4_m1_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -41,6 +59,7 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--mode", choices=["full", "kernel", "copy"], default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded "
@@ -56,17 +75,31 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.mode == "copy":
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {n} bytes x 20")
+        return
     info = _lib.device_info(0)
     log(f"device: {torch.cuda.get_device_name(0)} CUs={info.cu_count} sclk={info.sclk_khz / 1e3:.0f} MHz")
 
     # ---------------------------------------------------------------- weights (resident)
     L = args.layers
+    only = [p for p, (n, _, _) in enumerate(synth.LAYER) if n == "gate_up"] if args.mode == "kernel" else None
     layers = []
     codes0 = []  # host copy of layer 0 for the CPU baseline
     t0 = time.time()
     for l in range(L):
         projs = []
         for p, (name, K, N) in enumerate(synth.LAYER):
+            if only is not None and p not in only:
+                projs.append(None)
+                continue
             packed, codes, sc = synth.make_linear(N, K, 4, synth.linear_seed(l, p), device=dev)
             projs.append(ql.Weights.from_packed_device(4, K, N, packed, sc))
             if l == 0:
@@ -76,7 +109,7 @@ def main():
     torch.cuda.synchronize()
     log(f"{L} layers of W4 weights resident ({time.time() - t0:.1f} s)")
 
-    bytes_layer = sum(w.N * w.K // 2 + w.N * 4 for w in layers[0])
+    bytes_layer = sum(N * K // 2 + N * 4 for _, K, N in synth.LAYER)
     ws = ql.Workspace(512, 9728, 19456)
     acts = [synth.activations(1, K, seed=synth.linear_seed(0, p) + 1, device=dev)
             for p, (_, K, _) in enumerate(synth.LAYER)]
@@ -113,6 +146,13 @@ def main():
         e1.record(st)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3  # seconds
+
+    if args.mode == "kernel":
+        p = only[0]
+        g = capture(lambda i: ql.run(ws, layers[i % L][p], acts[p], out=outs[p], flags=flags[p]), L)
+        sec = time_graph(g, 10)
+        log(f"gate_up gemv: {sec * 1e6 / (10 * L):.2f} us/launch over {10 * L} launches")
+        return
 
     # ---------------------------------------------------------------- headline: decode layer
     # One graph = one pass over the L resident layers (4 launches each); the timed
@@ -222,7 +262,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": read_traffic(),
         },
         "cpu_baseline": cpu,
         "per_kernel_decode": per_kernel,

@@ -1,9 +1,10 @@
-"""Builds libqlinear.so (the HIP kernels and the C ABI) in-tree for gfx950.
+"""Builds libqlinear.so (the HIP kernels, the C ABI and the C++ npu mirror) in-tree
+for gfx950, and the native test binary tests/cpp/_build/npu_backend_test.
 
     python -m open_rknpu2_lm_infer_amd.build
 
-Every .hip file under csrc/ is compiled to an object in parallel with hipcc, then
-linked into open_rknpu2_lm_infer_amd/libqlinear.so next to this file.  Device code
+Every .hip / .cpp file under csrc/ is compiled to an object in parallel with hipcc,
+then linked into open_rknpu2_lm_infer_amd/libqlinear.so next to this file.  Device code
 is compiled with single-rounding IEEE semantics: no FP contraction, correctly
 rounded f32 divide and sqrt, denormals kept, packed-FP32 instructions disabled.
 """
@@ -35,15 +36,21 @@ COMMON = [
 ]
 
 
+ROOT = os.path.dirname(HERE)
+TEST_SRC = os.path.join(ROOT, "tests", "cpp", "npu_backend_test.cpp")
+TEST_BUILD = os.path.join(ROOT, "tests", "cpp", "_build")
+TEST_BIN = os.path.join(TEST_BUILD, "npu_backend_test")
+
+
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     objs, procs = [], []
     for src in sources():
-        obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
+        obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
         objs.append(obj)
         cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
         if verbose:
@@ -65,7 +72,19 @@ def build(verbose: bool = False) -> str:
            "-Wl,-rpath,/opt/rocm/lib"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_tests()
     return LIB
+
+
+def build_tests() -> str:
+    """Native test of the npu mirror; its checker (the CPU oracle) is compiled in."""
+    os.makedirs(TEST_BUILD, exist_ok=True)
+    oracle_obj = os.path.join(TEST_BUILD, "qlin_oracle.o")
+    subprocess.run(["gcc", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-std=c11", "-c",
+                    os.path.join(ROOT, "oracle", "qlin_oracle.c"), "-o", oracle_obj], check=True)
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", TEST_SRC, oracle_obj, "-o", TEST_BIN,
+                    f"-L{HERE}", "-lqlinear", "-Wl,-rpath,$ORIGIN/../../../open_rknpu2_lm_infer_amd", "-lm"], check=True)
+    return TEST_BIN
 
 
 if __name__ == "__main__":

@@ -1,0 +1,176 @@
+// Host-side mirror of the reference's npu::{Backend, Linear} over the C ABI.
+// See npu.hpp for the correspondence with src/npu.rs.
+#include "npu.hpp"
+
+#include <algorithm>
+#include <sstream>
+
+#include "../../include/qlinear.h"
+
+namespace npu {
+
+namespace {
+
+void check(int rc, const char* name) {
+    if (rc != QLIN_OK) throw Error(std::string(name) + ": " + qlin_strerror(rc) + " (" + std::to_string(rc) + ")", rc);
+}
+
+void ensure(bool ok, const char* msg) {
+    if (!ok) throw Error(msg, QLIN_ERR_PARAM);
+}
+
+}  // namespace
+
+size_t bucket(size_t rows) {
+    ensure(rows >= 1 && rows <= 256, "linear batch must be within 1..256");
+    if (rows <= 128) {
+        size_t p = 1;
+        while (p < rows) p <<= 1;
+        return p;
+    }
+    return (rows + 63) / 64 * 64;
+}
+
+struct Weights {
+    qlin_weights* raw = nullptr;
+    ~Weights() { qlin_weights_free(raw); }
+};
+
+struct Workspace {
+    qlin_workspace* raw = nullptr;
+    int max_k = 0, max_n = 0;
+    ~Workspace() { qlin_workspace_free(raw); }
+};
+
+struct Backend::Inner {
+    ModelOptions options;
+    uint32_t domain_id = 0;
+    std::map<size_t, std::unique_ptr<Workspace>> work;  // bucket rows -> workspace
+    int max_k = 0, max_n = 0;                           // largest loaded geometry
+    size_t loaded_w4 = 0, loaded_w8 = 0, geometries = 0;
+    uint64_t weight_bytes = 0;
+
+    Workspace* get_work(size_t m) {
+        auto it = work.find(m);
+        if (it != work.end() && it->second->max_k >= max_k && it->second->max_n >= max_n) return it->second.get();
+        auto ws = std::make_unique<Workspace>();
+        ws->max_k = max_k;
+        ws->max_n = max_n;
+        check(qlin_workspace_create((int32_t)m, max_k, max_n, &ws->raw), "create workspace");
+        Workspace* out = ws.get();
+        work[m] = std::move(ws);
+        return out;
+    }
+};
+
+struct Linear::State {
+    std::shared_ptr<Backend::Inner> owner;  // a Linear keeps its Backend alive (src/npu.rs:255-260)
+    std::unique_ptr<Weights> weights;
+    uint32_t bits = 0;
+    size_t k = 0, n = 0;
+};
+
+Backend Backend::create(const ModelOptions& options, uint32_t domain_id) {
+    ensure(options.chunk >= 1 && options.chunk <= 256, "ubatch-size must be within 1..256");
+    ensure(options.device >= 0, "invalid device");
+    Backend b;
+    b.inner = std::make_shared<Inner>();
+    b.inner->options = options;
+    b.inner->domain_id = domain_id;
+    return b;
+}
+
+Linear Backend::load(QuantMatrix matrix) {
+    // src/npu.rs:369-383
+    ensure(matrix.bits == 4 || matrix.bits == 8, "linear weights must use 4 or 8 bits");
+    ensure(matrix.k > 0 && matrix.n > 0 && matrix.k <= INT32_MAX && matrix.n <= INT32_MAX,
+           "invalid linear dimensions");
+    ensure(matrix.codes.size() == matrix.k * matrix.n && matrix.scales.size() == matrix.n,
+           "linear weight shape mismatch");
+    Linear lin;
+    lin.state = std::make_shared<Linear::State>();
+    lin.state->owner = inner;
+    lin.state->bits = matrix.bits;
+    lin.state->k = matrix.k;
+    lin.state->n = matrix.n;
+    lin.state->weights = std::make_unique<Weights>();
+    qlin_weight_config cfg{(int32_t)matrix.bits, (int32_t)matrix.k, (int32_t)matrix.n};
+    check(qlin_weights_create(&cfg, matrix.codes.data(), matrix.scales.data(), &lin.state->weights->raw),
+          matrix.bits == 4 ? "W4 weights" : "W8 weights");
+    qlin_weight_info info{};
+    check(qlin_weights_query(lin.state->weights->raw, &info), "weight query");
+    inner->weight_bytes += info.device_bytes;
+    (matrix.bits == 4 ? inner->loaded_w4 : inner->loaded_w8) += 1;
+    inner->geometries += 1;
+    inner->max_k = std::max(inner->max_k, (int)matrix.k);
+    inner->max_n = std::max(inner->max_n, (int)matrix.n);
+    inner->get_work(1);
+    matrix.codes.clear();  // the device copy is the only one kept (src/npu.rs:459-477)
+    matrix.codes.shrink_to_fit();
+    return lin;
+}
+
+void Backend::prepare(size_t rows) { inner->get_work(bucket(rows)); }
+
+void Backend::retain_workspaces(const std::vector<size_t>& rows) {
+    std::vector<size_t> keep;
+    for (size_t r : rows) keep.push_back(bucket(r));
+    for (auto it = inner->work.begin(); it != inner->work.end();) {
+        if (std::find(keep.begin(), keep.end(), it->first) == keep.end())
+            it = inner->work.erase(it);
+        else
+            ++it;
+    }
+}
+
+uint64_t Backend::weight_bytes() const { return inner->weight_bytes; }
+
+size_t Backend::tune_operations() const { return 0; }
+
+std::string Backend::stats() const {
+    uint64_t ws_bytes = 0;
+    for (auto& kv : inner->work) {
+        qlin_workspace_info info{};
+        if (qlin_workspace_query(kv.second->raw, &info) == QLIN_OK) ws_bytes += info.device_bytes;
+    }
+    std::ostringstream o;
+    o << "{\"backend\": \"qlinear-gfx950\", \"loaded_w4\": " << inner->loaded_w4
+      << ", \"loaded_w8\": " << inner->loaded_w8 << ", \"weight_payload_bytes\": " << inner->weight_bytes
+      << ", \"workspace_payload_bytes\": " << ws_bytes << ", \"workspace_count\": " << inner->work.size()
+      << ", \"tune_cache_hits\": 0, \"tune_cache_misses\": 0, \"tune_calls\": 0"
+      << ", \"strategy_fallbacks\": 0, \"strategy_fallback_calls\": 0, \"weight_reload_calls\": 0"
+      << ", \"weight_geometries\": " << inner->geometries << ", \"device\": " << inner->options.device
+      << ", \"domain_id\": " << inner->domain_id << "}";
+    return o.str();
+}
+
+size_t Linear::k() const { return state->k; }
+size_t Linear::n() const { return state->n; }
+
+void Linear::run(const float* input, size_t input_len, float* output, size_t output_len, size_t rows) const {
+    const size_t m = bucket(rows);
+    ensure(input_len >= rows * k() && output_len >= rows * n(), "linear input/output shape mismatch");
+    Workspace* ws = state->owner->get_work(m);
+    check(qlin_run_f32(ws->raw, state->weights->raw, (int32_t)rows, input, output),
+          state->bits == 4 ? "W4 run" : "W8 run");
+}
+
+bool Linear::run_swiglu(const float* input, size_t input_len, float* output, size_t output_len, size_t rows) const {
+    if (n() % 64 != 0) return false;
+    const size_t m = bucket(rows);
+    ensure(input_len >= rows * k() && output_len >= rows * (n() / 2), "linear input/output shape mismatch");
+    Workspace* ws = state->owner->get_work(m);
+    check(qlin_run_swiglu_f32(ws->raw, state->weights->raw, (int32_t)rows, input, output),
+          state->bits == 4 ? "W4 SwiGLU run" : "W8 SwiGLU run");
+    return true;
+}
+
+void Linear::run_device(const void* A, int a_dtype, int64_t lda, void* C, int c_dtype, int64_t ldc, size_t rows,
+                        uint32_t flags, void* stream) const {
+    ensure(rows >= 1 && rows <= INT32_MAX, "linear batch must be positive");
+    Workspace* ws = state->owner->get_work(std::max<size_t>(rows, 1));
+    check(qlin_run(ws->raw, state->weights->raw, (int32_t)rows, A, a_dtype, lda, C, c_dtype, ldc, flags, stream),
+          "device run");
+}
+
+}  // namespace npu

@@ -1,0 +1,101 @@
+"""Summaries of rocprofv3 result databases (SQLite, the default rocprofv3 output).
+
+    python -m open_rknpu2_lm_infer_amd.profsum stats  RESULTS.db [--match REGEX]
+    python -m open_rknpu2_lm_infer_amd.profsum pmc    RESULTS.db [--match REGEX]
+    python -m open_rknpu2_lm_infer_amd.profsum traffic --fetch F.db --write W.db \
+        --copy-fetch CF.db --copy-write CW.db --copy-bytes B --match REGEX
+
+`stats` prints per-kernel dispatch count and average / min / max duration;
+`pmc` prints the per-dispatch average of every collected counter; `traffic` turns
+FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the matched kernel into bytes per
+launch, each scaled by what the same counter reads for a plain copy of known size.
+"""
+from __future__ import annotations
+
+import argparse
+import re
+import sqlite3
+import sys
+
+
+def _con(path):
+    return sqlite3.connect(f"file:{path}?mode=ro", uri=True)
+
+
+def kernel_stats(path, match=None):
+    rows = _con(path).execute(
+        "select name, count(*), avg(duration), min(duration), max(duration), grid_x, workgroup_x, "
+        "vgpr_count, accum_vgpr_count, lds_size from kernels group by name, grid_x order by sum(duration) desc"
+    ).fetchall()
+    out = []
+    for name, n, avg, mn, mx, gx, wx, vgpr, agpr, lds in rows:
+        if match and not re.search(match, name):
+            continue
+        out.append(dict(name=name, dispatches=n, avg_us=avg / 1e3, min_us=mn / 1e3, max_us=mx / 1e3,
+                        workgroups=gx // max(wx, 1), wg_size=wx, vgpr=vgpr, agpr=agpr, lds=lds))
+    return out
+
+
+def pmc_means(path, match=None):
+    """{kernel name: {counter: mean value per dispatch}} (values summed over instances)."""
+    con = _con(path)
+    rows = con.execute(
+        "select name, dispatch_id, counter_name, sum(counter_value) from pmc_events "
+        "group by name, dispatch_id, counter_name").fetchall()
+    acc = {}
+    for name, _, cn, v in rows:
+        if match and not re.search(match, name):
+            continue
+        d = acc.setdefault(name, {}).setdefault(cn, [0.0, 0])
+        d[0] += v
+        d[1] += 1
+    return {k: {c: s / n for c, (s, n) in v.items()} for k, v in acc.items()}
+
+
+def _one(path, counter, match):
+    m = pmc_means(path, match)
+    vals = [v[counter] for v in m.values() if counter in v]
+    if not vals:
+        raise SystemExit(f"no {counter} for /{match}/ in {path}")
+    return sum(vals) / len(vals)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("what", choices=["stats", "pmc", "traffic"])
+    ap.add_argument("db", nargs="?")
+    ap.add_argument("--match", default=None)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-fetch")
+    ap.add_argument("--copy-write")
+    ap.add_argument("--copy-match", default="copyBuffer")
+    ap.add_argument("--copy-bytes", type=float)
+    a = ap.parse_args(argv)
+    if a.what == "stats":
+        for r in kernel_stats(a.db, a.match):
+            print(f"{r['avg_us']:9.2f} us avg  {r['min_us']:8.2f} min  {r['max_us']:8.2f} max  n={r['dispatches']:6d}  "
+                  f"wg={r['workgroups']}x{r['wg_size']} vgpr={r['vgpr']} lds={r['lds']}  {r['name'][:110]}")
+    elif a.what == "pmc":
+        for name, d in pmc_means(a.db, a.match).items():
+            print(name[:120])
+            for c, v in sorted(d.items()):
+                print(f"    {c:32s} {v:16.2f}")
+    else:
+        f_k = _one(a.fetch, "FETCH_SIZE", a.match)
+        w_k = _one(a.write, "WRITE_SIZE", a.match)
+        f_c = _one(a.copy_fetch, "FETCH_SIZE", a.copy_match)
+        w_c = _one(a.copy_write, "WRITE_SIZE", a.copy_match)
+        kib = a.copy_bytes / 1024.0
+        f_scale, w_scale = kib / f_c, kib / w_c
+        fetch_b = f_k * f_scale * 1024.0
+        write_b = w_k * w_scale * 1024.0
+        print(f"copy of {a.copy_bytes:.0f} B: FETCH_SIZE {f_c:.1f} KiB (scale {f_scale:.4f}), "
+              f"WRITE_SIZE {w_c:.1f} KiB (scale {w_scale:.4f})")
+        print(f"kernel /{a.match}/: FETCH_SIZE {f_k:.1f} KiB -> {fetch_b:.0f} B, WRITE_SIZE {w_k:.1f} KiB -> {write_b:.0f} B")
+        print(f"traffic_bytes_per_launch: {fetch_b + write_b:.0f}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
