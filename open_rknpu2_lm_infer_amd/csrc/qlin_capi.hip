@@ -29,7 +29,7 @@ struct qlin_workspace {
     int32_t* gemv_part;  // [kGemvMaxRows, max_np], zero at rest
     uint32_t* counters;  // [n_counters], zero at rest
     int n_counters;
-    int32_t* gemm_part;  // [kGemmPartTiles * 64 * 256]
+    int32_t* gemm_part;  // [kGemmPartInts]
     uint32_t* err;       // sticky error word
     float* dA;           // host-API staging [max_rows, max_k]
     float* dC;           // host-API staging [max_rows, max_n]
@@ -40,8 +40,8 @@ struct qlin_workspace {
 
 namespace {
 
-constexpr int kGemmPartTiles = 512;  // max tiles x splits of one split-K launch
-constexpr int kGemmTile = 128;
+constexpr int64_t kGemmPartInts = 16 << 20;  // split-K partial buffer: 64 MiB of int32
+constexpr int kGemmTileM = 128, kGemmTileK = 128;
 
 int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
@@ -272,7 +272,7 @@ int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_w
     const size_t bq = (size_t)max_rows * ws->max_kp, bs = (size_t)max_rows * sizeof(float);
     const size_t bgp = (size_t)kGemvMaxRows * ws->max_np * sizeof(int32_t);
     const size_t bc = (size_t)ws->n_counters * sizeof(uint32_t);
-    const size_t bgm = (size_t)kGemmPartTiles * 64 * 256 * sizeof(int32_t);
+    const size_t bgm = (size_t)kGemmPartInts * sizeof(int32_t);
     const size_t bA = (size_t)max_rows * max_k * sizeof(float), bC = (size_t)max_rows * max_n * sizeof(float);
     bool ok = hipMalloc(&ws->q, bq) == hipSuccess && hipMalloc(&ws->s, bs) == hipSuccess &&
               hipMalloc(&ws->gemv_part, bgp) == hipSuccess && hipMalloc(&ws->counters, bc) == hipSuccess &&
@@ -417,23 +417,28 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     p.ldc = ldc;
     p.c_kind = c_kind;
     p.flags = flags;
-    p.m_tiles = (rows + kGemmTile - 1) / kGemmTile;
-    p.n_tiles = sw ? (w->N / 2 + 63) / 64 : (w->N + kGemmTile - 1) / kGemmTile;
-    const int ktiles = w->Kp / kGemmTile;
+    const int bn = gemm_tile_n(w->bits, w->N);
+    const int cols = sw ? bn / 2 : bn;  // output channels per tile
+    p.m_tiles = (rows + kGemmTileM - 1) / kGemmTileM;
+    p.n_tiles = ((sw ? w->N / 2 : w->N) + cols - 1) / cols;
+    const int ktiles = w->Kp / kGemmTileK;
     const int tiles = p.m_tiles * p.n_tiles;
+    const int64_t slice = (int64_t)gemm_regs_per_thread(bn) * 256;  // ints of one partial tile
     int S = env_int("QLIN_GEMM_SPLITS", 0);
     if (S <= 0) {
+        // split K until the grid covers the CUs, keeping >= 4 k tiles per split
         const int target = env_int("QLIN_GEMM_TARGET_WGS", ws->cu_count);
         S = (target + tiles / 2) / tiles;
         S = std::min(S, std::max(1, ktiles / 4));
     }
     S = std::max(1, std::min(S, ktiles));
-    while (S > 1 && (tiles * S > kGemmPartTiles || tiles > ws->n_counters)) --S;
+    while (S > 1 && ((int64_t)tiles * S * slice > kGemmPartInts || tiles > ws->n_counters)) --S;
     p.ktiles_per_split = (ktiles + S - 1) / S;
     p.splits = (ktiles + p.ktiles_per_split - 1) / p.ktiles_per_split;
+    p.group_m = std::max(1, std::min(p.m_tiles, env_int("QLIN_GEMM_GROUP_M", 4)));
     p.part = ws->gemm_part;
     p.counters = ws->counters;
-    return launch_gemm(p, w->bits, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+    return launch_gemm(p, w->bits, bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
 int check_run(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags) {
