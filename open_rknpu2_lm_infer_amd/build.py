@@ -36,6 +36,11 @@ COMMON = [
 ]
 
 
+# Per-file additions.  The GEMM keeps its MFMA accumulators in VGPRs: with the
+# compiler's AGPR heuristics the two-tile unrolled k loop re-shuffled the accumulator
+# registers on every iteration.
+FILE_FLAGS = {"qlin_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 ROOT = os.path.dirname(HERE)
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "npu_backend_test.cpp")
 TEST_BUILD = os.path.join(ROOT, "tests", "cpp", "_build")
@@ -52,7 +57,7 @@ def build(verbose: bool = False) -> str:
     for src in sources():
         obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
         objs.append(obj)
-        cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+        cmd = [HIPCC, *COMMON, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

@@ -427,13 +427,18 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     int S = env_int("QLIN_GEMM_SPLITS", 0);
     if (S <= 0) {
         // split K until the grid covers the CUs, keeping >= 4 k tiles per split
+        // split-K's partial round trip costs more than a second resident workgroup
+        // per CU gains, so the target is one workgroup per CU
         const int target = env_int("QLIN_GEMM_TARGET_WGS", ws->cu_count);
         S = (target + tiles / 2) / tiles;
         S = std::min(S, std::max(1, ktiles / 4));
     }
     S = std::max(1, std::min(S, ktiles));
     while (S > 1 && ((int64_t)tiles * S * slice > kGemmPartInts || tiles > ws->n_counters)) --S;
-    p.ktiles_per_split = (ktiles + S - 1) / S;
+    // the GEMM's k loop takes two tiles per iteration: Kp is a multiple of 256, so
+    // ktiles is even, and an even split size keeps every split's count even
+    if (ktiles % 2) return QLIN_ERR_PARAM;
+    p.ktiles_per_split = ((ktiles + S - 1) / S + 1) & ~1;
     p.splits = (ktiles + p.ktiles_per_split - 1) / p.ktiles_per_split;
     p.group_m = std::max(1, std::min(p.m_tiles, env_int("QLIN_GEMM_GROUP_M", 4)));
     p.part = ws->gemm_part;

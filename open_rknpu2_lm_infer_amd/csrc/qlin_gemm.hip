@@ -3,22 +3,25 @@
 // int32 reduce (QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:28-31); gfx950 multiplies
 // the int8 codes directly, so no digit split or correction term is needed.
 //
-// Tile 128 (rows) x BN (channels, 128 or 256) x 128 (k); 256 threads as 2 x 2 waves,
+// Tile 128 (rows) x BN (channels) x 128 (k); 256 threads as 2 x 2 waves,
 // each wave 64 x BN/2 = 4 x BN/32 tiles of v_mfma_i32_16x16x64_i8 per 64-k half.
 //
-// Operands.  Quantized rows (A) and codes (B) go global -> registers -> LDS.  W4
-// codes stay packed in LDS (half the LDS traffic of unpacked codes) and are unpacked
-// per fragment: w & 0xF0 and (w << 4) & 0xF0 are 16*code as exact int8 values, in
-// odd-k / even-k byte order, so the A rows are stored in LDS with each 8-byte group
-// reordered evens-then-odds to match.  The int32 sums then carry a factor 16 that is
-// shifted out exactly before the epilogue.  LDS granules are XOR-swizzled by row so
-// the 16 rows one quarter-wave reads fall in distinct banks.
+// Operands go from global memory straight into LDS (buffer_load_dwordx4 ... lds):
+// one instruction fills 1 KiB of LDS in lane order, and which global 16-byte chunk a
+// lane fetches sets the XOR swizzle that keeps fragment reads free of bank conflicts.
+// A row beyond M or N lies past its buffer descriptor's size and arrives as zero.
+// W4 codes stay packed in LDS; one 16-byte read gives a lane 32 codes, the k group it
+// multiplies in both 64-k halves of the tile.  They are unpacked per fragment:
+// w & 0xF0 and (w << 4) & 0xF0 are 16*code as exact int8 values in odd-k / even-k
+// order, and the activation fragment is reordered evens-then-odds in registers to
+// match.  The int32 sums carry a factor 16 that is shifted out exactly at the end.
 //
-// Pipeline.  Two register buffers keep the global loads of k tiles t+1 and t+2 in
-// flight while tile t is multiplied from one of two LDS buffers; one barrier per k
-// tile.  All loads are unconditional (tile indices clamp at the end), so the compiler
-// waits for exactly the tile it stores.  The k loop is unrolled by two so every LDS
-// address is a per-lane base plus an immediate offset.
+// Pipeline.  NST LDS stages: the copy of k tile t + NST - 1 is issued while tile t is
+// multiplied.  Within a tile, the fragments of the second 64-k half are read while
+// the first half's MFMAs run, and those of the next tile (after the one barrier per
+// tile) while the second half's run.  Every k range has an even number of tiles (Kp is
+// a multiple of 256 and splits are even), so the loop is unrolled by two with the two
+// B fragment sets swapping roles and no register moves.
 //
 // SwiGLU: a tile of BN/2 output channels j loads B rows j (gate) and N/2 + j (up);
 // each wave keeps gate and up accumulators for the same (row, j) in the same lane.
@@ -34,60 +37,91 @@ namespace qlin {
 
 constexpr int BM = 128, BK = 128;
 constexpr int kGemmThreads = 256;
+constexpr int kLdsBytes = 160 * 1024;  // LDS of one gfx950 CU
 
-template <int BITS, int BN>
+// W4 stages are 24 KiB: three of them let two workgroups share a CU, so one's MFMAs
+// run while the other waits on LDS.  W8 stages are 32 KiB: one workgroup, four stages.
+template <int BITS, int BN, int NSTAGES = (BITS == 4 ? 3 : 4)>
 struct GemmGeom {
-    static constexpr int WN = BN / 2;                       // columns per wave
-    static constexpr int NI = WN / 16;                      // B fragments per wave
-    static constexpr int MI = 4;                            // A fragments per wave (64 rows)
-    static constexpr int A_BYTES = BM * BK;                 // 16 KiB
-    static constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;   // bytes of one B row in LDS
+    static constexpr int NI = BN / 32;                         // B fragments per wave
+    static constexpr int A_BYTES = BM * BK;                    // 16 KiB
+    static constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;      // bytes of one B row
     static constexpr int B_BYTES = BN * B_ROW;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS = 2 * STAGE;
-    static constexpr int NA = A_BYTES / 16 / kGemmThreads;  // 16-byte A loads per thread per k tile
-    static constexpr int NB = B_BYTES / 16 / kGemmThreads;  // 16-byte B loads per thread per k tile
-    static constexpr int REGS = MI * NI * 4;                // int32 accumulators per lane
+    static constexpr int NST = kLdsBytes / STAGE < NSTAGES ? kLdsBytes / STAGE : NSTAGES;  // stages
+    static constexpr int LDS = NST * STAGE;
+    static constexpr int NA = A_BYTES / 1024 / 4;              // 1 KiB copies per wave per stage
+    static constexpr int NB = B_BYTES / 1024 / 4;
+    static constexpr int NL = NA + NB;
+    static constexpr int REGS = 4 * NI * 4;                    // int32 accumulators per lane
+    static_assert(NST >= 3, "pipeline needs three LDS stages");
 };
 
-__device__ __forceinline__ uint4 evens_odds(uint4 v) {
-    // [k0..k7 | k8..k15] -> [k0 k2 k4 k6 k1 k3 k5 k7 | k8 ...]
-    uint4 r;
-    r.x = __builtin_amdgcn_perm(v.y, v.x, 0x06040200u);
-    r.y = __builtin_amdgcn_perm(v.y, v.x, 0x07050301u);
-    r.z = __builtin_amdgcn_perm(v.w, v.z, 0x06040200u);
-    r.w = __builtin_amdgcn_perm(v.w, v.z, 0x07050301u);
-    return r;
-}
-
-// LDS offsets.  A and W8 B rows: 128 bytes as 8 chunks of 16 swizzled by row & 7.
-// W4 B rows: 64 bytes as 8 granules of 8 swizzled by (row & 7) ^ ((row >> 3) & 1).
-__device__ __forceinline__ int off16(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
-__device__ __forceinline__ int off8(int row, int g) { return row * 64 + ((g ^ (row & 7) ^ ((row >> 3) & 1)) << 3); }
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 word 3)
-
-// Buffer loads: a per-tile descriptor whose size covers only the tile's valid rows,
-// a per-lane row offset (VGPR) and the k offset in an SGPR.  A row beyond M or N lies
-// past the descriptor's size and reads as zero, so every load is unconditional.
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t rows, int64_t ld) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(rows * ld), kBufferFlags);
 }
 
-template <int BITS, bool SWIGLU, int BN>
-struct Src {
-    using G = GemmGeom<BITS, BN>;
-    __amdgpu_buffer_rsrc_t ra, rg, ru;  // A rows; B (gate) rows; B up rows (SwiGLU)
-    int aoff[G::NA], boff[G::NB];
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-    __device__ __forceinline__ Src(const GemmParams& p, int m0, int n0) {
-        const int tid = threadIdx.x;
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_block, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_block, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// Workgroup barrier without a memory fence: the caller's explicit waits have already
+// completed the LDS reads and copies it orders (a fence would also wait for the copies
+// still meant to be in flight).  The empty asm statements keep the compiler from
+// moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ v4i evens_odds(v4i v) {
+    // [k0..k7 | k8..k15] -> [k0 k2 k4 k6 | k1 k3 k5 k7 | k8 k10 .. | k9 k11 ..]
+    v4i r;
+    r[0] = (int)__builtin_amdgcn_perm((unsigned)v[1], (unsigned)v[0], 0x06040200u);
+    r[1] = (int)__builtin_amdgcn_perm((unsigned)v[1], (unsigned)v[0], 0x07050301u);
+    r[2] = (int)__builtin_amdgcn_perm((unsigned)v[3], (unsigned)v[2], 0x06040200u);
+    r[3] = (int)__builtin_amdgcn_perm((unsigned)v[3], (unsigned)v[2], 0x07050301u);
+    return r;
+}
+
+// 16 packed codes (8 bytes) -> 16*code as int8, evens then odds per 8-code group
+__device__ __forceinline__ v4i unpack_w4(int x, int y) {
+    const unsigned ux = (unsigned)x, uy = (unsigned)y;
+    return v4i{(int)((ux << 4) & 0xF0F0F0F0u), (int)(ux & 0xF0F0F0F0u), (int)((uy << 4) & 0xF0F0F0F0u),
+               (int)(uy & 0xF0F0F0F0u)};
+}
+
+template <bool SWIGLU, int BN>
+__device__ __forceinline__ constexpr int b_frag_row(int wn, int j) {
+    constexpr int NI = BN / 32;
+    if constexpr (SWIGLU) return (j >= NI / 2 ? BN / 2 : 0) + wn * (BN / 4) + (j % (NI / 2)) * 16;
+    return wn * (BN / 2) + j * 16;
+}
+
+// Global -> LDS copy plan of one wave: NA activation blocks of 8 rows x 128 bytes and
+// NB weight blocks (W8: 8 rows x 128 bytes; W4: 16 rows x 64 bytes).
+template <int BITS, bool SWIGLU, int BN>
+struct Copy {
+    using G = GemmGeom<BITS, BN>;
+    __amdgpu_buffer_rsrc_t ra, rg, ru;
+    int aoff[G::NA], boff[G::NB];
+    int wave;
+
+    __device__ __forceinline__ Copy(const GemmParams& p, int m0, int n0, int wave_, int lane) : wave(wave_) {
         ra = tile_rsrc(p.q + (int64_t)m0 * p.ldq, min(p.M - m0, BM), p.ldq);
         if constexpr (SWIGLU) {
             const int nh = p.N >> 1, rows = min(nh - n0, BN / 2);
@@ -99,103 +133,132 @@ struct Src {
         }
 #pragma unroll
         for (int i = 0; i < G::NA; ++i) {
-            const int c = tid + kGemmThreads * i;
-            aoff[i] = (c >> 3) * (int)p.ldq + 16 * (c & 7);
+            const int row = (wave * G::NA + i) * 8 + (lane >> 3);
+            aoff[i] = row * (int)p.ldq + (((lane & 7) ^ (row & 7)) << 4);
         }
 #pragma unroll
         for (int i = 0; i < G::NB; ++i) {
-            const int c = tid + kGemmThreads * i;
-            int row = BITS == 8 ? (c >> 3) : (c >> 2);
-            const int ch = BITS == 8 ? (c & 7) : (c & 3);
-            if (SWIGLU && i >= G::NB / 2) row -= BN / 2;  // load i < NB/2 covers gate rows [0, BN/2)
-            boff[i] = row * (int)p.wrow + 16 * ch;
-        }
-    }
-};
-
-template <int BITS, bool SWIGLU, int BN>
-struct Stage {
-    using G = GemmGeom<BITS, BN>;
-    uint4 ra[G::NA], rb[G::NB];
-
-    // The scheduler barriers keep each stage's loads together and in program order:
-    // the memory counter retires in issue order, so a stage stored while the other is
-    // still in flight waits only for its own loads.
-    __device__ __forceinline__ void load(const Src<BITS, SWIGLU, BN>& s, int kt) {
-        const int k0 = kt * BK;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < G::NA; ++i) ra[i] = bload16(s.ra, s.aoff[i], k0);
-#pragma unroll
-        for (int i = 0; i < G::NB; ++i)
-            rb[i] = bload16(SWIGLU && i >= G::NB / 2 ? s.ru : s.rg, s.boff[i], BITS == 8 ? k0 : k0 / 2);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    __device__ __forceinline__ void store(uint8_t* As, uint8_t* Bs) const {
-        const int tid = threadIdx.x;
-#pragma unroll
-        for (int i = 0; i < G::NA; ++i) {
-            const int c = tid + kGemmThreads * i, row = c >> 3, ch = c & 7;
-            uint4 v = ra[i];
-            if constexpr (BITS == 4) v = evens_odds(v);
-            *reinterpret_cast<uint4*>(As + off16(row, ch)) = v;
-        }
-#pragma unroll
-        for (int i = 0; i < G::NB; ++i) {
-            const int c = tid + kGemmThreads * i;
+            const int blk = wave * G::NB + i;
             if constexpr (BITS == 8) {
-                *reinterpret_cast<uint4*>(Bs + off16(c >> 3, c & 7)) = rb[i];
+                int row = blk * 8 + (lane >> 3);
+                const int chunk = (lane & 7) ^ (row & 7);
+                if (SWIGLU && row >= BN / 2) row -= BN / 2;
+                boff[i] = row * (int)p.wrow + (chunk << 4);
             } else {
-                const int row = c >> 2, ch = c & 3;  // 16 packed bytes = granules 2ch, 2ch+1
-                *reinterpret_cast<uint2*>(Bs + off8(row, 2 * ch)) = make_uint2(rb[i].x, rb[i].y);
-                *reinterpret_cast<uint2*>(Bs + off8(row, 2 * ch + 1)) = make_uint2(rb[i].z, rb[i].w);
+                int row = blk * 16 + (lane >> 2);
+                const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+                if (SWIGLU && row >= BN / 2) row -= BN / 2;
+                boff[i] = row * (int)p.wrow + (chunk << 4);
             }
         }
     }
+
+    // copy k tile kt into the stage at LDS byte offset `stage`
+    __device__ __forceinline__ void issue(uint8_t* smem, int stage, int kt) const {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < G::NA; ++i) dma16(ra, smem + stage + (wave * G::NA + i) * 1024, aoff[i], k0);
+#pragma unroll
+        for (int i = 0; i < G::NB; ++i) {
+            const int blk = wave * G::NB + i;
+            const int rows_per_blk = BITS == 8 ? 8 : 16;
+            const bool up = SWIGLU && blk * rows_per_blk >= BN / 2;
+            dma16(up ? ru : rg, smem + stage + G::A_BYTES + blk * 1024, boff[i], BITS == 8 ? k0 : k0 / 2);
+        }
+    }
 };
 
-template <bool SWIGLU, int BN>
-__device__ __forceinline__ int b_frag_row(int wn, int ni) {
+// Fragment registers of one k tile: packed or int8 weight fragments for both halves.
+template <int BITS, int BN>
+struct BFrag {
+    v4i v[BITS == 4 ? BN / 32 : 2 * (BN / 32)];
+};
+
+template <int BITS, bool SWIGLU, int BN>
+__device__ __forceinline__ void read_b(BFrag<BITS, BN>& b, const uint8_t* sb, int bbase0, int bbase1, int wn) {
     constexpr int NI = BN / 32;
-    if constexpr (SWIGLU) return (ni >= NI / 2 ? BN / 2 : 0) + wn * (BN / 4) + (ni % (NI / 2)) * 16;
-    return wn * (BN / 2) + ni * 16;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        if constexpr (BITS == 4) {
+            b.v[j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN>(wn, j) * 64);
+        } else {
+            b.v[2 * j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN>(wn, j) * 128);
+            b.v[2 * j + 1] = *reinterpret_cast<const v4i*>(sb + bbase1 + b_frag_row<SWIGLU, BN>(wn, j) * 128);
+        }
+    }
 }
 
-template <int BITS, bool SWIGLU, int BN>
-__device__ __forceinline__ void mma_tile(v4i (&acc)[4][BN / 32], const uint8_t* As, const uint8_t* Bs,
-                                         const int (&abase)[2], const int (&bbase)[2], int wn) {
-    using G = GemmGeom<BITS, BN>;
+__device__ __forceinline__ void read_a(v4i (&a)[4], const uint8_t* sa, int abase) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        v4i a[4];
+    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4i*>(sa + abase + i * 16 * 128);
+}
+
+template <int BITS, int BN>
+__device__ __forceinline__ void mma_half(v4i (&acc)[4][BN / 32], const v4i (&a)[4], const BFrag<BITS, BN>& b, int h) {
+    constexpr int NI = BN / 32;
+    v4i ap[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4i*>(As + abase[h] + i * 16 * 128);
+    for (int i = 0; i < 4; ++i) ap[i] = BITS == 4 ? evens_odds(a[i]) : a[i];
 #pragma unroll
-        for (int j = 0; j < G::NI; ++j) {
-            v4i b;
-            if constexpr (BITS == 8) {
-                b = *reinterpret_cast<const v4i*>(Bs + bbase[h] + b_frag_row<SWIGLU, BN>(wn, j) * 128);
-            } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(Bs + bbase[h] + b_frag_row<SWIGLU, BN>(wn, j) * 64);
-                b[0] = (int)((w.x << 4) & 0xF0F0F0F0u);  // k 0 2 4 6
-                b[1] = (int)(w.x & 0xF0F0F0F0u);         // k 1 3 5 7
-                b[2] = (int)((w.y << 4) & 0xF0F0F0F0u);
-                b[3] = (int)(w.y & 0xF0F0F0F0u);
-            }
+    for (int j = 0; j < NI; ++j) {
+        const v4i w = BITS == 4 ? (h == 0 ? unpack_w4(b.v[j][0], b.v[j][1]) : unpack_w4(b.v[j][2], b.v[j][3]))
+                                : b.v[2 * j + h];
+        // weights as the first operand: the 16x16 result is transposed, so each lane
+        // holds 4 consecutive output channels of one row
 #pragma unroll
-            // weights as the first operand: the 16x16 result is transposed, so each lane
-            // holds 4 consecutive output channels of one row
-            for (int i = 0; i < 4; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a[i], acc[i][j], 0, 0, 0);
-        }
+        for (int i = 0; i < 4; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, ap[i], acc[i][j], 0, 0, 0);
     }
+}
+
+// Instruction interleave for the scheduler: MFMA i is followed by one LDS read while
+// any remain (first NDS), one global-to-LDS copy while any remain (first NVM) and
+// VALU instructions.  A wave issues in order and stalls behind an MFMA the matrix
+// core cannot yet take, so reads and copies placed after a run of MFMAs would wait
+// for the whole run; spread out, they issue while the MFMAs execute.
+template <int I, int NMFMA, int NDS, int NVM, int NVALU>
+__device__ __forceinline__ void interleave() {
+    if constexpr (I < NMFMA) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (I < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if constexpr (I < NVM) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+        if constexpr (NVALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
+        interleave<I + 1, NMFMA, NDS, NVM, NVALU>();
+    }
+}
+
+// One k tile: multiply tile t (its first-half A fragments in a0, B in bc); read its
+// second-half A fragments, then, after the barrier, the next tile's first-half A and
+// its B fragments into bn.
+template <int BITS, bool SWIGLU, int BN>
+__device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], v4i (&a1)[4], const BFrag<BITS, BN>& bc,
+                                          BFrag<BITS, BN>& bn, const Copy<BITS, SWIGLU, BN>& cp, uint8_t* smem, int t,
+                                          int kt_begin, int last, int abase0, int abase1, int bbase0, int bbase1, int wn) {
+    using G = GemmGeom<BITS, BN>;
+    constexpr int NMFMA = 4 * G::NI;                          // per half
+    constexpr int NREAD_B = BITS == 4 ? G::NI : 2 * G::NI;     // 16-byte B reads per tile
+    constexpr int NVALU = BITS == 4 ? 2 : 1;                   // unpack / permute work per MFMA
+    const uint8_t* s0 = smem + (t % G::NST) * G::STAGE;
+    read_a(a1, s0, abase1);
+    mma_half<BITS, BN>(acc, a0, bc, 0);
+    interleave<0, NMFMA, 4, 0, NVALU>();
+    wait_lgkm0();
+    wait_vm<(G::NST - 3) * G::NL>();  // own copies of tile t+1 have landed
+    barrier_no_fence();               // everyone's have, and stage t-1 is free
+    const int fill = t + G::NST - 1;
+    cp.issue(smem, (fill % G::NST) * G::STAGE, min(kt_begin + fill, last));
+    const uint8_t* s1 = smem + ((t + 1) % G::NST) * G::STAGE;
+    read_a(a0, s1, abase0);
+    read_b<BITS, SWIGLU, BN>(bn, s1 + G::A_BYTES, bbase0, bbase1, wn);
+    mma_half<BITS, BN>(acc, a1, bc, 1);
+    interleave<0, NMFMA, 4 + NREAD_B, G::NL, NVALU>();
 }
 
 template <int BITS, bool SWIGLU, int OUT, int BN>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     using G = GemmGeom<BITS, BN>;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 15, fc = lane >> 4;
 
@@ -216,20 +279,15 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
     const int ktiles = p.Kp / BK;
     const int kt_begin = z * p.ktiles_per_split;
     const int kt_end = min(kt_begin + p.ktiles_per_split, ktiles);
-    const int T = kt_end - kt_begin;
+    const int T = kt_end - kt_begin;  // even and >= 2
+    const int last = kt_end - 1;
 
-    uint8_t* A0 = smem;
-    uint8_t* B0 = smem + G::A_BYTES;
-    uint8_t* A1 = smem + G::STAGE;
-    uint8_t* B1 = smem + G::STAGE + G::A_BYTES;
-
-    // per-lane LDS bases of the fragments (row & 7 == fr & 7 for every fragment row)
-    int abase[2], bbase[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        abase[h] = off16(wm * 64 + fr, h * 4 + fc);
-        bbase[h] = BITS == 8 ? off16(fr, h * 4 + fc) : off8(fr, h * 4 + fc);
-    }
+    // fragment read offsets: lane (fr, fc) multiplies k bytes [32 fc + 16 h, +16) of
+    // the tile in half h, from rows whose low bits are those of fr
+    const int abase0 = (wm * 64 + fr) * 128 + (((2 * fc) ^ (fr & 7)) << 4);
+    const int abase1 = (wm * 64 + fr) * 128 + (((2 * fc + 1) ^ (fr & 7)) << 4);
+    const int bbase0 = BITS == 4 ? fr * 64 + ((fc ^ ((fr >> 1) & 3)) << 4) : fr * 128 + (((2 * fc) ^ (fr & 7)) << 4);
+    const int bbase1 = BITS == 4 ? 0 : fr * 128 + (((2 * fc + 1) ^ (fr & 7)) << 4);
 
     v4i acc[4][G::NI];
 #pragma unroll
@@ -237,28 +295,25 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int j = 0; j < G::NI; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-    if (T > 0) {
-        // s0 / s1 carry k tiles t+2 / t+3 from global memory while tile t is multiplied;
-        // past the end the tile index clamps, and the surplus tiles go to an LDS buffer
-        // that is not read again.
-        const int last = kt_end - 1;
-        const Src<BITS, SWIGLU, BN> src(p, m0, n0);
-        Stage<BITS, SWIGLU, BN> s0, s1;
-        s0.load(src, kt_begin);
-        s1.load(src, min(kt_begin + 1, last));
-        s0.store(A0, B0);
-        s0.load(src, min(kt_begin + 2, last));
-        __syncthreads();
+    {
+        const Copy<BITS, SWIGLU, BN> cp(p, m0, n0, wave, lane);
+#pragma unroll
+        for (int s = 0; s < G::NST - 1; ++s) cp.issue(smem, s * G::STAGE, min(kt_begin + s, last));
+        wait_vm<(G::NST - 2) * G::NL>();
+        barrier_no_fence();
+
+        v4i a0[4], a1[4];
+        BFrag<BITS, BN> bx, by;
+        read_a(a0, smem, abase0);
+        read_b<BITS, SWIGLU, BN>(bx, smem + G::A_BYTES, bbase0, bbase1, wn);
+
         for (int t = 0; t < T; t += 2) {
-            mma_tile<BITS, SWIGLU, BN>(acc, A0, B0, abase, bbase, wn);  // tile t
-            s1.store(A1, B1);                                           // tile t+1
-            s1.load(src, min(kt_begin + t + 3, last));
-            __syncthreads();
-            if (t + 1 < T) mma_tile<BITS, SWIGLU, BN>(acc, A1, B1, abase, bbase, wn);
-            s0.store(A0, B0);                                           // tile t+2
-            s0.load(src, min(kt_begin + t + 4, last));
-            __syncthreads();
+            gemm_step<BITS, SWIGLU, BN>(acc, a0, a1, bx, by, cp, smem, t, kt_begin, last, abase0, abase1, bbase0, bbase1, wn);
+            gemm_step<BITS, SWIGLU, BN>(acc, a0, a1, by, bx, cp, smem, t + 1, kt_begin, last, abase0, abase1, bbase0, bbase1, wn);
         }
+        // drain the surplus copies before the LDS is reused or the workgroup ends
+        wait_vm<0>();
+        __syncthreads();
     }
 
     if (p.splits > 1) {
@@ -273,7 +328,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
                     store_coherent(mine + ((i * G::NI + j) * 4 + r) * kGemmThreads + tid, acc[i][j][r]);
         wait_all_memory();
         __syncthreads();
-        int* flag = reinterpret_cast<int*>(smem);
+        int* flag = reinterpret_cast<int*>(smem);  // the LDS stages are drained
         if (tid == 0) flag[0] = atomicAdd(&p.counters[tile], 1u) == (unsigned)(p.splits - 1);
         __syncthreads();
         if (!flag[0]) return;
@@ -383,9 +438,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
 
 template <int BITS, bool SWIGLU, int OUT, int BN>
 static hipError_t launch_gemm_t(const GemmParams& p, hipStream_t stream) {
+    using G = GemmGeom<BITS, BN>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_kernel<BITS, SWIGLU, OUT, BN>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    if (attr != hipSuccess) return attr;
     dim3 grid(p.m_tiles * p.n_tiles * p.splits), block(kGemmThreads);
-    constexpr size_t lds = GemmGeom<BITS, BN>::LDS;
-    gemm_kernel<BITS, SWIGLU, OUT, BN><<<grid, block, lds, stream>>>(p);
+    gemm_kernel<BITS, SWIGLU, OUT, BN><<<grid, block, G::LDS, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -397,17 +456,14 @@ static hipError_t launch_gemm_b(const GemmParams& p, hipStream_t stream) {
     return p.c_kind == 1 ? launch_gemm_t<BITS, false, 1, BN>(p, stream) : launch_gemm_t<BITS, false, 0, BN>(p, stream);
 }
 
-int gemm_tile_n(int bits, int N) {
-    // W4 takes 256-channel tiles (packed codes keep the LDS stage at 32 KiB) when N
-    // has enough of them; W8 and narrow W4 linears take 128.
-    return (bits == 4 && N >= 4096) ? 256 : 128;
-}
+int gemm_tile_n(int, int) { return 128; }
+
 
 int gemm_regs_per_thread(int bn) { return 4 * (bn / 32) * 4; }
 
 hipError_t launch_gemm(const GemmParams& p, int bits, int bn, hipStream_t stream) {
-    if (bits == 4) return bn == 256 ? launch_gemm_b<4, 256>(p, stream) : launch_gemm_b<4, 128>(p, stream);
-    return launch_gemm_b<8, 128>(p, stream);
+    if (bn != 128) return hipErrorInvalidValue;
+    return bits == 4 ? launch_gemm_b<4, 128>(p, stream) : launch_gemm_b<8, 128>(p, stream);
 }
 
 }  // namespace qlin

@@ -90,7 +90,7 @@ int gemv_pick_waves(int groups, int steps);
 bool gemv_can_fuse(int M, int K, int waves, bool norm);
 size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm);
 hipError_t launch_gemm(const GemmParams& p, int bits, int bn, hipStream_t stream);
-int gemm_tile_n(int bits, int N);          // channels of B per workgroup tile (128 or 256)
+int gemm_tile_n(int bits, int N);          // channels of B per workgroup tile
 int gemm_regs_per_thread(int bn);          // int32 accumulators per thread of one tile
 hipError_t launch_pack_w4(const int8_t* codes_nk, int N, int K, int Np, int Kp, uint8_t* out,
                           hipStream_t stream);
