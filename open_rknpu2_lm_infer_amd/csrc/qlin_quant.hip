@@ -1,8 +1,11 @@
 // Kernel (a): per-token activation quantization, optionally after RMSNorm.
 //
-// One 256-thread workgroup per row.  Pass 1 (absmax + finiteness, with the norm
-// applied on the fly) and pass 2 (quantize, 8 values per thread per iteration,
-// one 64-bit store) read the row from global memory; the second read hits L1/L2.
+// Without RMSNorm, rows of up to 40960 fp16 / 20480 f32 values are quantized from
+// registers by four waves each.  Otherwise one 256-thread workgroup takes a row: rows of up to
+// 60 KiB are copied into LDS once and every pass reads them there; longer rows take
+// the two-pass kernel, whose pass 1
+// (absmax + finiteness, with the norm applied on the fly) and pass 2 (quantize, 8
+// values per thread per iteration, one 64-bit store) read global memory.
 // The replaced library stage is the CPU scan + quantize of rk_npu_w4a8_quant.cpp
 // (QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:26-27); the arithmetic is the oracle's,
 // src/npu.rs:1101-1110.
@@ -51,11 +54,285 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(QuantParams p) 
     }
 }
 
+// Row staged in LDS: one coalesced read of the row from global memory; the statistics
+// and the quantize pass then read LDS.  Rows of up to kStageBytes take this path (the
+// default 64 KiB workgroup LDS limit, less the static reduction words).  Needs
+// K % 8 == 0 and a 16-byte aligned row (16-byte copies).
+constexpr int kStageBytes = 60 * 1024;
+
+template <typename T>
+__device__ __forceinline__ float lds_ld(const T* r, int i) {
+    if constexpr (sizeof(T) == 2) return __half2float(r[i]);
+    else return r[i];
+}
+
+// 8 consecutive values from LDS at a 16-byte aligned element index
+template <typename T>
+__device__ __forceinline__ void lds_ld8(const T* r, int k0, float v[8]) {
+    if constexpr (sizeof(T) == 2) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(r + k0);
+        const __half2* h = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float2 f = __half22float2(h[i]);
+            v[2 * i] = f.x;
+            v[2 * i + 1] = f.y;
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(r + k0);
+        const float4 b = *reinterpret_cast<const float4*>(r + k0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void quant_rows_staged_kernel(QuantParams p) {
+    extern __shared__ __align__(16) uint8_t stage[];
+    __shared__ float red[8];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const T* x = reinterpret_cast<const T*>(p.A) + (int64_t)row * p.lda;
+    T* xs = reinterpret_cast<T*>(stage);
+    constexpr int E = 16 / sizeof(T);  // elements per 16-byte copy
+    const int nchunks = p.K / E;
+    // eight 16-byte loads in flight per thread before any is stored.  Loads and stores
+    // are unconditional: past the end a lane copies the last chunk onto itself (same
+    // data), so no load waits behind a branch.
+    constexpr int B = 8;
+    for (int c0 = t; c0 < nchunks; c0 += kRowThreads * B) {
+        uint4 v[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) v[i] = reinterpret_cast<const uint4*>(x)[min(c0 + i * kRowThreads, nchunks - 1)];
+#pragma unroll
+        for (int i = 0; i < B; ++i) reinterpret_cast<uint4*>(xs)[min(c0 + i * kRowThreads, nchunks - 1)] = v[i];
+    }
+    __syncthreads();
+
+    float nscale = 1.0f;
+    if (p.gamma) {
+        // RMSNorm scale with the reference's summation order (see block_rms_scale)
+        if (p.flags & kFlagNormSeq) {
+            if (t == 0) {
+                float sum = 0.0f;
+                for (int i = 0; i < p.K; ++i) {
+                    const float v = lds_ld(xs, i);
+                    const float v2 = v * v;
+                    sum = sum + v2;
+                }
+                red[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+            }
+        } else if (t < 64) {
+            float acc = 0.0f;
+            const int j = t & 15;
+            if (t < 16) {
+                const int n16 = p.K & ~15;
+                for (int i = 0; i < n16; i += 16) {
+                    const float v = lds_ld(xs, i + j);
+                    acc = __builtin_fmaf(v, v, acc);
+                }
+            }
+            const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
+            const float tj = (acc + b) + (c + d);
+            const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
+            if (t == 0) {
+                float sum = (tj + t1) + (t2 + t3);
+                for (int i = p.K & ~15; i < p.K; ++i) {
+                    const float v = lds_ld(xs, i);
+                    const float v2 = v * v;
+                    sum = sum + v2;
+                }
+                red[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+            }
+        }
+        __syncthreads();
+        nscale = red[0];
+        __syncthreads();
+    }
+
+    // absmax (after the norm) and finiteness (of the input), 8 values per step
+    const bool gvec = (reinterpret_cast<uintptr_t>(p.gamma) & 15) == 0;
+    float m = 0.0f;
+    int f = 0;
+    for (int k0 = t * 8; k0 < p.K; k0 += kRowThreads * 8) {
+        float v[8];
+        lds_ld8(xs, k0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f |= !__builtin_isfinite(v[i]);
+        if (p.gamma) {
+            float g[8];
+            load8_gamma(p.gamma, k0, p.K, gvec, g);
+            apply_norm8(v, g, nscale);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    }
+    block_max_or(m, f, red);
+    const float s = qscale_from_absmax(m);
+    const float inv = 1.0f / s;
+    const bool rne = (p.flags & kFlagRne) != 0;
+    int8_t* qrow = p.q + (int64_t)row * p.ldq;
+    // 8 codes per step; the zero tail [K, ldq) too (ldq % 8 == 0 on this path)
+    for (int k0 = t * 8; k0 < p.ldq; k0 += kRowThreads * 8) {
+        uint32_t w0 = 0, w1 = 0;
+        if (k0 < p.K) {
+            float v[8];
+            lds_ld8(xs, k0, v);
+            if (p.gamma) {
+                float g[8];
+                load8_gamma(p.gamma, k0, p.K, gvec, g);
+                apply_norm8(v, g, nscale);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w0 |= (uint32_t)(quant_one(v[i], inv, rne) & 0xff) << (8 * i);
+                w1 |= (uint32_t)(quant_one(v[4 + i], inv, rne) & 0xff) << (8 * i);
+            }
+        }
+        *reinterpret_cast<uint2*>(qrow + k0) = make_uint2(w0, w1);
+    }
+    if (t == 0) {
+        p.s[row] = s;
+        if (f && p.err) atomicOr(p.err, 1u);
+    }
+}
+
+// Without RMSNorm: WPR waves per row (1 or 4) and 4 / WPR rows per 256-thread
+// workgroup, the row held in registers (NC 16-byte chunks per lane, all loaded
+// before any is used).  Absmax and finiteness come from one integer max over the
+// sign-masked bit patterns: for non-negative fp16 / f32 values the bit order is the
+// value order, and Inf / NaN are exactly the patterns at or above the all-ones
+// exponent.  Needs K % 8 == 0, a 16-byte aligned row and an 8-byte aligned q with
+// ldq % 8 == 0.
+template <typename T, int NC, int WPR>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(QuantParams p, int rows) {
+    __shared__ uint32_t red[4];
+    constexpr int L = 64 * WPR;  // lanes per row
+    const int lane = threadIdx.x % L;
+    const int row = blockIdx.x * (4 / WPR) + threadIdx.x / L;
+    if (WPR == 1 && row >= rows) return;  // whole wave; WPR 4 grids are exact
+    constexpr int E = 16 / sizeof(T);
+    const T* x = reinterpret_cast<const T*>(p.A) + (int64_t)row * p.lda;
+    const int nchunks = p.K / E;
+    uint4 raw[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) raw[i] = reinterpret_cast<const uint4*>(x)[min(lane + L * i, nchunks - 1)];
+    // (clamped chunks repeat the last chunk: harmless for a max)
+    uint32_t mx = 0;
+    constexpr uint32_t kAbs = sizeof(T) == 2 ? 0x7FFF7FFFu : 0x7FFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const uint32_t w[4] = {raw[i].x & kAbs, raw[i].y & kAbs, raw[i].z & kAbs, raw[i].w & kAbs};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (sizeof(T) == 2) mx = max(mx, max(w[j] & 0xFFFFu, w[j] >> 16));
+            else mx = max(mx, w[j]);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    if constexpr (WPR > 1) {
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = max(max(red[0], red[1]), max(red[2], red[3]));
+    }
+    float m;
+    bool bad;
+    if constexpr (sizeof(T) == 2) {
+        bad = mx >= 0x7C00u;
+        m = __half2float(__ushort_as_half((unsigned short)mx));
+    } else {
+        bad = mx >= 0x7F800000u;
+        m = __uint_as_float(mx);
+    }
+    if (bad) {
+        // rare: a row holding Inf / NaN takes the fmaxf absmax of the other kernels
+        // (NaN ignored, Inf kept); the row is reported through the error word
+        float fm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const T* e = reinterpret_cast<const T*>(&raw[i]);
+#pragma unroll
+            for (int j = 0; j < E; ++j) fm = fmaxf(fm, fabsf(lds_ld(e, j)));
+        }
+        fm = wave_max(fm);
+        if constexpr (WPR > 1) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = __float_as_uint(fm);
+            __syncthreads();
+            fm = fmaxf(fmaxf(__uint_as_float(red[0]), __uint_as_float(red[1])),
+                       fmaxf(__uint_as_float(red[2]), __uint_as_float(red[3])));
+        }
+        m = fm;
+    }
+    const float s = qscale_from_absmax(m);
+    const float inv = 1.0f / s;
+    const bool rne = (p.flags & kFlagRne) != 0;
+    int8_t* qrow = p.q + (int64_t)row * p.ldq;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + L * i;
+        if (c < nchunks) {
+            const T* e = reinterpret_cast<const T*>(&raw[i]);
+            uint32_t w[E / 4];
+#pragma unroll
+            for (int g = 0; g < E / 4; ++g) {
+                w[g] = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    w[g] |= (uint32_t)(quant_one(lds_ld(e, 4 * g + j), inv, rne) & 0xff) << (8 * j);
+            }
+            if constexpr (E == 8)
+                *reinterpret_cast<uint2*>(qrow + c * E) = make_uint2(w[0], w[1]);
+            else
+                *reinterpret_cast<uint32_t*>(qrow + c * E) = w[0];
+        }
+    }
+    for (int k0 = p.K + 8 * lane; k0 < p.ldq; k0 += 8 * L) *reinterpret_cast<uint2*>(qrow + k0) = make_uint2(0, 0);
+    if (lane == 0) {
+        p.s[row] = s;
+        if (bad && p.err) atomicOr(p.err, 1u);
+    }
+}
+
+template <typename T, int WPR>
+static bool launch_quant_reg_w(const QuantParams& p, int rows, hipStream_t stream) {
+    constexpr int E = 16 / sizeof(T);
+    const int per_lane = (p.K / E + 64 * WPR - 1) / (64 * WPR);
+    dim3 grid((rows + 4 / WPR - 1) / (4 / WPR)), block(256);
+    if (per_lane <= 2) quant_rows_reg_kernel<T, 2, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else if (per_lane <= 4) quant_rows_reg_kernel<T, 4, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else if (per_lane <= 8) quant_rows_reg_kernel<T, 8, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else if (per_lane <= 12) quant_rows_reg_kernel<T, 12, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else if (per_lane <= 20) quant_rows_reg_kernel<T, 20, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else return false;
+    return true;
+}
+
+// Four waves per row measured faster than one at 512 and 4096 rows (more waves in
+// flight, a quarter of the per-lane work).
+template <typename T>
+static bool launch_quant_reg(const QuantParams& p, int rows, hipStream_t stream) {
+    return launch_quant_reg_w<T, 4>(p, rows, stream);
+}
+
 hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     const bool vec = ((reinterpret_cast<uintptr_t>(p.A) & 15) == 0) && (p.lda % 8 == 0) &&
                      (p.K % 8 == 0);
     dim3 grid(rows), block(kRowThreads);
+    const size_t row_bytes = (size_t)p.K * (p.a_f16 ? 2 : 4);
+    const bool qvec = ((reinterpret_cast<uintptr_t>(p.q) & 7) == 0) && (p.ldq % 8 == 0);
+    if (vec && qvec && !p.gamma) {
+        const bool ok = p.a_f16 ? launch_quant_reg<__half>(p, rows, stream) : launch_quant_reg<float>(p, rows, stream);
+        if (ok) return hipGetLastError();
+    }
+    if (vec && qvec && row_bytes <= (size_t)kStageBytes) {
+        if (p.a_f16)
+            quant_rows_staged_kernel<__half><<<grid, block, row_bytes, stream>>>(p);
+        else
+            quant_rows_staged_kernel<float><<<grid, block, row_bytes, stream>>>(p);
+        return hipGetLastError();
+    }
     if (p.a_f16) {
         if (vec)
             hipLaunchKernelGGL((quant_rows_kernel<__half, true>), grid, block, 0, stream, p);
