@@ -183,6 +183,48 @@ int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* weights, int32_t 
                        const int8_t* q, int64_t ldq, const float* s, void* C, int32_t c_dtype,
                        int64_t ldc, uint32_t flags, void* stream);
 
+/* ---- decode chain: several linears in one launch (1..4 rows, fp16 activations) ----
+ * Replaces the per-projection calls of the decode step, src/model/dense.rs:398-540
+ * (Cpu::norm, then Projection::run / run_swiglu for qkv, o, gate_up, down, layer
+ * after layer).  Each stage computes exactly what qlin_run_rmsnorm (gamma != NULL)
+ * or qlin_run (gamma == NULL) computes for its input, with fp16 in and out: the
+ * chain output equals those calls made one after another.  Attention, RoPE and the
+ * residual adds are not part of it; a stage reads an earlier stage's output (or the
+ * chain input) from a column offset, so a caller can route e.g. the q columns of qkv
+ * into o. */
+typedef struct qlin_chain qlin_chain;
+
+typedef struct qlin_chain_stage {
+    const qlin_weights* weights;
+    uint32_t flags;       /* QLIN_SWIGLU, QLIN_ROUND_HALF_EVEN, QLIN_NORM_SEQUENTIAL */
+    const float* gamma;   /* device RMSNorm weights [K], 16-byte aligned, or NULL */
+    float eps;
+    int32_t input;        /* -1: the chain input; j >= 0: the output of stage j (j < this) */
+    int32_t input_offset; /* first column taken from that output (multiple of 8) */
+} qlin_chain_stage;
+
+/* Checks the stages (K of each stage = the columns it reads; K % 8 == 0) and
+ * allocates the intermediate fp16 buffers for max_rows <= 4 rows.  The weights must
+ * outlive the chain. */
+int qlin_chain_create(const qlin_chain_stage* stages, int32_t n_stages, int32_t max_rows,
+                      qlin_chain** out);
+void qlin_chain_free(qlin_chain* chain);
+
+/* x: device fp16 [rows, ldx] (K of stage 0 columns, 16-byte aligned rows); y: device
+ * fp16 [rows, ldy] gets the last stage's output.  Asynchronous on `stream`. */
+int qlin_chain_run(qlin_chain* chain, int32_t rows, const void* x, int64_t ldx, void* y, int64_t ldy,
+                   void* stream);
+
+/* Device pointer and row stride (elements) of stage `stage`'s fp16 output from the
+ * last run (the last stage writes y instead). */
+int qlin_chain_stage_output(const qlin_chain* chain, int32_t stage, void** ptr, int64_t* ld);
+
+/* Error word of the runs since the last clear: QLIN_OK, QLIN_ERR_NONFINITE (an input
+ * row held Inf/NaN) or QLIN_ERR_DEVICE (a stage wait gave up: the grid was not fully
+ * resident, e.g. other work occupied the GPU; the outputs are then invalid).
+ * Synchronizes the last run's stream.  clear != 0 resets the word. */
+int qlin_chain_status(qlin_chain* chain, int32_t clear);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,11 @@ SIGNATURES = {
     "qlin_quantize": (ctypes.c_int, [_I32, _I32, _P, _I32, _I64, _P, _F, _P, _I64, _P, _P, _U32, _P]),
     "qlin_gemm_i32": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _I64, _P]),
     "qlin_run_quantized": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _P, _I32, _I64, _U32, _P]),
+    "qlin_chain_create": (ctypes.c_int, [_P, _I32, _I32, _P]),
+    "qlin_chain_free": (None, [_P]),
+    "qlin_chain_run": (ctypes.c_int, [_P, _I32, _P, _I64, _P, _I64, _P]),
+    "qlin_chain_stage_output": (ctypes.c_int, [_P, _I32, _P, _P]),
+    "qlin_chain_status": (ctypes.c_int, [_P, _I32]),
 }
 
 
@@ -74,6 +79,11 @@ class WorkspaceInfo(ctypes.Structure):
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("device", _I32), ("cu_count", _I32), ("arch", _I32), ("reserved", _I32),
                 ("sclk_khz", _I64), ("mclk_khz", _I64), ("bus_width_bits", _I64), ("hbm_bytes", _I64)]
+
+
+class ChainStage(ctypes.Structure):
+    _fields_ = [("weights", _P), ("flags", _U32), ("gamma", _P), ("eps", _F), ("input", _I32),
+                ("input_offset", _I32)]
 
 
 class QlinError(RuntimeError):

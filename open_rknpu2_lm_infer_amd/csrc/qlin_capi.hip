@@ -559,3 +559,174 @@ int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* w, int32_t rows, 
 }
 
 }  // extern "C"
+
+// ---- decode chain --------------------------------------------------------------
+
+#include "qlin_chain.hpp"
+
+struct qlin_chain {
+    int n, max_rows, device, grid;
+    int x_cols;        // chain-input columns read by the stages
+    int last_cols;     // output columns of the last stage
+    int kp_max, k_max;
+    size_t lds, q_bytes, red_bytes;
+    std::vector<ChainStage> stages;  // host copy
+    std::vector<int> cols;           // output columns per stage
+    ChainStage* d_stages;
+    std::vector<_Float16*> outs;     // per stage, null for the last
+    std::vector<int64_t> ld;
+    uint32_t* counters;
+    uint32_t* err;
+    hipStream_t last;
+};
+
+void qlin_chain_free(qlin_chain* c) {
+    if (!c) return;
+    if (c->last) (void)hipStreamSynchronize(c->last);
+    for (auto* o : c->outs) (void)hipFree(o);
+    (void)hipFree(c->d_stages);
+    (void)hipFree(c->counters);
+    (void)hipFree(c->err);
+    delete c;
+}
+
+int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, qlin_chain** out) {
+    if (!out) return QLIN_ERR_PARAM;
+    *out = nullptr;
+    if (!st || n < 1 || max_rows < 1 || max_rows > 4) return QLIN_ERR_PARAM;
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    auto* c = new (std::nothrow) qlin_chain();
+    if (!c) return QLIN_ERR_NOMEM;
+    c->n = n;
+    c->max_rows = max_rows;
+    c->device = dev;
+    c->stages.resize(n);
+    c->cols.resize(n);
+    c->outs.assign(n, nullptr);
+    c->ld.assign(n, 0);
+    const uint32_t allowed = QLIN_SWIGLU | QLIN_ROUND_HALF_EVEN | QLIN_NORM_SEQUENTIAL;
+    int rc = QLIN_OK;
+    for (int s = 0; s < n && rc == QLIN_OK; ++s) {
+        const qlin_chain_stage& d = st[s];
+        const qlin_weights* w = d.weights;
+        if (!w || w->device != dev || (d.flags & ~allowed) || w->K % 8 || d.input < -1 || d.input >= s ||
+            d.input_offset < 0 || d.input_offset % 8 || (s == 0 && d.input != -1)) {
+            rc = QLIN_ERR_PARAM;
+            break;
+        }
+        if ((d.flags & QLIN_SWIGLU) && w->N % 64) {
+            rc = QLIN_ERR_UNSUPPORTED;
+            break;
+        }
+        if (d.gamma && (!(d.eps > 0.0f && std::isfinite(d.eps)) || (reinterpret_cast<uintptr_t>(d.gamma) & 15))) {
+            rc = QLIN_ERR_PARAM;
+            break;
+        }
+        c->cols[s] = (d.flags & QLIN_SWIGLU) ? w->N / 2 : w->N;
+        if (d.input == -1) {
+            c->x_cols = std::max(c->x_cols, d.input_offset + w->K);
+        } else if (d.input_offset + w->K > c->cols[d.input]) {
+            rc = QLIN_ERR_PARAM;
+            break;
+        }
+        ChainStage& cs = c->stages[s];
+        cs.W = w->W;
+        cs.wscale = w->scales;
+        cs.wrow = w->wrow;
+        cs.bits = w->bits;
+        cs.K = w->K;
+        cs.Kp = w->Kp;
+        cs.N = w->N;
+        cs.Np = w->Np;
+        cs.flags = (int)(d.flags & (kFlagSwiglu | kFlagRne | kFlagNormSeq));
+        cs.groups = ((d.flags & QLIN_SWIGLU) ? w->N / 2 : w->Np) / 16;
+        cs.gamma = d.gamma;
+        cs.eps = d.eps;
+        cs.x_offset = d.input == -1 ? d.input_offset : 0;
+        c->kp_max = std::max(c->kp_max, w->Kp);
+        c->k_max = std::max(c->k_max, w->K);
+    }
+    if (rc == QLIN_OK) {
+        c->last_cols = c->cols[n - 1];
+        c->lds = chain_lds_bytes(max_rows, c->kp_max, c->k_max, &c->q_bytes, &c->red_bytes);
+        if (c->lds > (size_t)kChainMaxLds) rc = QLIN_ERR_UNSUPPORTED;
+    }
+    // one workgroup per CU; every workgroup must be resident for the stage waits
+    if (rc == QLIN_OK && chain_resident_per_cu(max_rows, c->lds) < 1) rc = QLIN_ERR_UNSUPPORTED;
+    c->grid = cu_count(dev);
+    for (int s = 0; s < n - 1 && rc == QLIN_OK; ++s) {
+        c->ld[s] = round_up(c->cols[s], 8);
+        if (hipMalloc(&c->outs[s], (size_t)max_rows * c->ld[s] * sizeof(_Float16)) != hipSuccess) rc = QLIN_ERR_NOMEM;
+    }
+    for (int s = 0; s < n && rc == QLIN_OK; ++s) {
+        ChainStage& cs = c->stages[s];
+        const int in = st[s].input;
+        cs.in = in >= 0 ? reinterpret_cast<const __half*>(c->outs[in]) + st[s].input_offset : nullptr;
+        cs.ld_in = in >= 0 ? c->ld[in] : 0;
+        cs.out = c->outs[s];
+        cs.ld_out = c->ld[s];
+    }
+    if (rc == QLIN_OK &&
+        (hipMalloc(&c->d_stages, sizeof(ChainStage) * n) != hipSuccess ||
+         hipMalloc(&c->counters, sizeof(uint32_t) * n) != hipSuccess || hipMalloc(&c->err, sizeof(uint32_t)) != hipSuccess))
+        rc = QLIN_ERR_NOMEM;
+    if (rc == QLIN_OK &&
+        (hipMemcpy(c->d_stages, c->stages.data(), sizeof(ChainStage) * n, hipMemcpyHostToDevice) != hipSuccess ||
+         hipMemset(c->counters, 0, sizeof(uint32_t) * n) != hipSuccess || hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess ||
+         hipDeviceSynchronize() != hipSuccess))
+        rc = QLIN_ERR_DEVICE;
+    if (rc != QLIN_OK) {
+        qlin_chain_free(c);
+        return rc;
+    }
+    *out = c;
+    return QLIN_OK;
+}
+
+int qlin_chain_run(qlin_chain* c, int32_t rows, const void* x, int64_t ldx, void* y, int64_t ldy, void* stream) {
+    if (!c || rows < 1 || rows > c->max_rows || !x || !y || ldx < c->x_cols || ldx % 8 ||
+        (reinterpret_cast<uintptr_t>(x) & 15) || ldy < c->last_cols || (reinterpret_cast<uintptr_t>(y) & 1))
+        return QLIN_ERR_PARAM;
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    if (dev != c->device) return QLIN_ERR_PARAM;
+    ChainParams p{};
+    p.stages = c->d_stages;
+    p.n_stages = c->n;
+    p.M = rows;
+    p.x = reinterpret_cast<const __half*>(x);
+    p.ldx = ldx;
+    p.y = reinterpret_cast<_Float16*>(y);
+    p.ldy = ldy;
+    p.counters = c->counters;
+    p.err = c->err;
+    p.spin_limit = env_int("QLIN_CHAIN_SPIN_LIMIT", 1 << 22);  // ~0.2 s of polling per wait
+    p.kp_max = c->kp_max;
+    p.lds_q_bytes = (int)c->q_bytes;
+    p.lds_red_bytes = (int)c->red_bytes;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    c->last = st;
+    return launch_chain(p, c->grid, c->lds, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+int qlin_chain_stage_output(const qlin_chain* c, int32_t stage, void** ptr, int64_t* ld) {
+    if (!c || !ptr || !ld || stage < 0 || stage >= c->n - 1) return QLIN_ERR_PARAM;
+    *ptr = c->outs[stage];
+    *ld = c->ld[stage];
+    return QLIN_OK;
+}
+
+int qlin_chain_status(qlin_chain* c, int32_t clear) {
+    if (!c) return QLIN_ERR_PARAM;
+    if (hipStreamSynchronize(c->last) != hipSuccess) return QLIN_ERR_DEVICE;
+    uint32_t e = 0;
+    if (hipMemcpy(&e, c->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (e & 2u) {
+        // a wait gave up: the counters may be left mid-count; restart them from zero
+        if (hipMemset(c->counters, 0, sizeof(uint32_t) * c->n) != hipSuccess) return QLIN_ERR_DEVICE;
+    }
+    if (clear && e && hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess) return QLIN_ERR_DEVICE;
+    if (hipDeviceSynchronize() != hipSuccess) return QLIN_ERR_DEVICE;
+    return (e & 2u) ? QLIN_ERR_DEVICE : (e ? QLIN_ERR_NONFINITE : QLIN_OK);
+}

@@ -97,6 +97,69 @@ class Workspace:
             pass
 
 
+class _DeviceArray:
+    """__cuda_array_interface__ view of library-owned device memory."""
+
+    def __init__(self, ptr: int, shape, strides, typestr: str):
+        self.__cuda_array_interface__ = {"shape": tuple(shape), "strides": tuple(strides), "typestr": typestr,
+                                         "data": (ptr, False), "version": 2}
+
+
+class Chain:
+    """Decode chain (qlin_chain): several linears in one persistent launch, 1..4 rows of
+    fp16 activations.  stages: dicts with weights (Weights), flags, gamma (device f32
+    [K] or None), eps, input (-1 = chain input, j = output of stage j; default: the
+    previous stage) and offset (first column read)."""
+
+    def __init__(self, stages: list, max_rows: int = 1):
+        arr = (_lib.ChainStage * len(stages))()
+        self._keep = []
+        for i, st in enumerate(stages):
+            g = st.get("gamma")
+            arr[i] = _lib.ChainStage(st["weights"].handle, st.get("flags", 0), g.data_ptr() if g is not None else None,
+                                     st.get("eps", 1e-6), st.get("input", -1 if i == 0 else i - 1), st.get("offset", 0))
+            self._keep.append(st["weights"])
+            if g is not None:
+                self._keep.append(g)
+        self.handle = ctypes.c_void_p()
+        check(_lib.load().qlin_chain_create(arr, len(stages), max_rows, ctypes.byref(self.handle)),
+              "qlin_chain_create")
+        self.cols = [st["weights"].N // 2 if st.get("flags", 0) & QLIN_SWIGLU else st["weights"].N for st in stages]
+        self.max_rows = max_rows
+
+    def run(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        M = x.shape[0]
+        if out is None:
+            out = torch.empty((M, self.cols[-1]), dtype=torch.float16, device=x.device)
+        assert x.dtype == torch.float16 and out.dtype == torch.float16 and x.stride(1) == 1 and out.stride(1) == 1
+        check(_lib.load().qlin_chain_run(self.handle, M, _ptr(x), x.stride(0), _ptr(out), out.stride(0), _stream()),
+              "qlin_chain_run")
+        return out
+
+    def stage_output(self, stage: int, rows: int) -> torch.Tensor:
+        """Copy of stage `stage`'s output from the last run (not the last stage)."""
+        ptr, ld = ctypes.c_void_p(), ctypes.c_int64()
+        check(_lib.load().qlin_chain_stage_output(self.handle, stage, ctypes.byref(ptr), ctypes.byref(ld)),
+              "qlin_chain_stage_output")
+        view = torch.as_tensor(_DeviceArray(ptr.value, (rows, self.cols[stage]), (2 * ld.value, 2), "<f2"),
+                               device=torch.device("cuda", torch.cuda.current_device()))
+        return view.clone()
+
+    def status(self, clear: bool = True) -> int:
+        return _lib.load().qlin_chain_status(self.handle, int(clear))
+
+    def close(self):
+        if self.handle:
+            _lib.load().qlin_chain_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def run(ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor | None = None,
         out_dtype=torch.float16, flags: int = 0, gamma: torch.Tensor | None = None,
         eps: float = 1e-6) -> torch.Tensor:

@@ -16,6 +16,8 @@ Activations: N(0,1) with 1% of the K channels (seeded choice) scaled by 20.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 BASE_SEED = 42
@@ -87,9 +89,23 @@ def layer_bits(name: str, mixed: bool) -> int:
     return 4
 
 
-def make_linear(N: int, K: int, bits: int, seed: int, device="cpu"):
-    """(packed device layout, codes [N,K] int8, scales [N]) for one linear."""
+def stack_scales(N: int, K: int, bits: int, seed: int, device="cpu") -> torch.Tensor:
+    """Per-channel scales for a layer stack: W4 as in scales(); W8 variance preserving,
+    U(0.5, 1.5) / (73 sqrt(K)) (73 ~ the std of uniform [-127, 127] codes), so an
+    un-normalized W8 input (o, down) keeps its magnitude instead of growing ~50x per
+    projection and overflowing fp16 a layer later.  The stack workload names no W8
+    scale range; the single-linear U(0.002, 0.02) is kept for single linears."""
+    if bits == 4:
+        return scales(N, bits, seed, device)
+    g = gen(seed, device)
+    u = torch.rand((N,), generator=g, device=device, dtype=torch.float32) + 0.5
+    return u / (73.0 * math.sqrt(K))
+
+
+def make_linear(N: int, K: int, bits: int, seed: int, device="cpu", stack: bool = False):
+    """(packed device layout, codes [N,K] int8, scales [N]) for one linear; stack=True
+    draws W8 scales from stack_scales()."""
     c = codes(N, K, bits, seed, device)
-    s = scales(N, bits, seed + 7, device)
+    s = stack_scales(N, K, bits, seed + 7, device) if stack else scales(N, bits, seed + 7, device)
     packed = pack_w4(c) if bits == 4 else c.contiguous()
     return packed, c, s

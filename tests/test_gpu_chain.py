@@ -1,0 +1,203 @@
+"""Decode chain (qlin_chain_*): several linears in one persistent launch.
+
+Each stage must equal the single-linear entry point (qlin_run / qlin_run_rmsnorm)
+applied to that stage's input, bit for bit in fp16: the chain fuses launches, not
+arithmetic.  Stage inputs are taken from the chain's own previous outputs, so each
+stage is checked on exactly what it consumed.  Against the oracle, each stage is
+checked with the same bar as the single linear (plain outputs bit-exact, SwiGLU
+within 1e-3 relative in fp16).
+"""
+import numpy as np
+import pytest
+import torch
+
+from open_rknpu2_lm_infer_amd import qlinear as ql
+from open_rknpu2_lm_infer_amd import synth
+from open_rknpu2_lm_infer_amd._lib import QLIN_ERR_NONFINITE, QLIN_ERR_PARAM, QLIN_ERR_UNSUPPORTED, QlinError
+from tests.test_gpu_parity import check_outputs, f16_bits, oracle_linear
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ws():
+    w = ql.Workspace(16, 9728, 19456)
+    yield w
+    w.close()
+
+
+def linear(bits, K, N, seed, stack=False):
+    packed, codes, sc = synth.make_linear(N, K, bits, seed, stack=stack)
+    w = ql.Weights.from_packed_device(bits, K, N, packed.to(DEV), sc.to(DEV))
+    return w, codes.numpy(), sc.numpy()
+
+
+def stage_inputs(chain, stages, x, y, rows):
+    """Input of every stage as the chain saw it, from its own outputs."""
+    outs = [chain.stage_output(s, rows) for s in range(len(stages) - 1)] + [y]
+    ins = []
+    for st in stages:
+        src = x if st["input"] == -1 else outs[st["input"]]
+        ins.append(src[:, st["offset"]:st["offset"] + st["weights"].K].contiguous())
+    return ins, outs
+
+
+def check_against_single(ws, chain, stages, x, y, rows):
+    ins, outs = stage_inputs(chain, stages, x, y, rows)
+    for s, st in enumerate(stages):
+        ref = ql.run(ws, st["weights"], ins[s], out_dtype=torch.float16, flags=st.get("flags", 0),
+                     gamma=st.get("gamma"), eps=st.get("eps", 1e-6))
+        torch.cuda.synchronize()
+        g, e = f16_bits(outs[s]), f16_bits(ref)
+        bad = np.argwhere(g != e)
+        assert len(bad) == 0, f"stage {s}: {len(bad)} fp16 mismatches, first {bad[:3].tolist()}"
+    return ins, outs
+
+
+def build_small(seed0):
+    w0 = linear(4, 512, 768, seed0)
+    w1 = linear(8, 256, 512, seed0 + 1)
+    w2 = linear(4, 512, 1024, seed0 + 2)
+    w3 = linear(8, 512, 320, seed0 + 3)
+    w4 = linear(4, 256, 96, seed0 + 4)
+    g0 = synth.gamma(512, seed=seed0 + 5).to(DEV)
+    g2 = synth.gamma(512, seed=seed0 + 6).to(DEV)
+    stages = [
+        dict(weights=w0[0], flags=0, gamma=g0, eps=1e-6, input=-1, offset=0),
+        dict(weights=w1[0], flags=0, input=0, offset=128),
+        dict(weights=w2[0], flags=ql.QLIN_SWIGLU, gamma=g2, eps=1e-6, input=1, offset=0),
+        dict(weights=w3[0], flags=0, input=2, offset=0),
+        dict(weights=w4[0], flags=0, input=-1, offset=256),
+    ]
+    host = [w0, w1, w2, w3, w4]
+    return stages, host
+
+
+@pytest.mark.parametrize("rows", [1, 3, 4])
+def test_chain_small_matches_single_linears(oracle, ws, rows):
+    stages, host = build_small(900)
+    chain = ql.Chain(stages, max_rows=4)
+    x = synth.activations(rows, 512, seed=901 + rows, device=DEV)
+    y = chain.run(x)
+    torch.cuda.synchronize()
+    assert chain.status() == 0
+    ins, outs = check_against_single(ws, chain, stages, x, y, rows)
+    # and each stage against the oracle on its own input
+    for s, st in enumerate(stages):
+        _, codes, sc = host[s]
+        g = st.get("gamma")
+        expect = oracle_linear(oracle, ins[s].cpu(), codes, sc, bool(st["flags"] & ql.QLIN_SWIGLU),
+                               gamma=None if g is None else g.cpu().numpy())
+        check_outputs(oracle, outs[s], expect, bool(st["flags"] & ql.QLIN_SWIGLU), torch.float16)
+    chain.close()
+
+
+def qwen_layer_stages(layer, gammas):
+    """qkv (W4, RMSNorm) -> o (W8, the q columns of qkv) -> gate_up (W4, RMSNorm, SwiGLU)
+    -> down (W8): the mixed W4/W8 decode layer with attention left out (stack scales)."""
+    (_, Kq, Nq), (_, Ko, No), (_, Kg, Ng), (_, Kd, Nd) = synth.LAYER
+    wq = linear(4, Kq, Nq, synth.linear_seed(layer, 0), stack=True)
+    wo = linear(8, Ko, No, synth.linear_seed(layer, 1), stack=True)
+    wg = linear(4, Kg, Ng, synth.linear_seed(layer, 2), stack=True)
+    wd = linear(8, Kd, Nd, synth.linear_seed(layer, 3), stack=True)
+    base = 4 * layer
+    stages = [
+        dict(weights=wq[0], flags=0, gamma=gammas[0], eps=1e-6, input=base - 1 if layer else -1, offset=0),
+        dict(weights=wo[0], flags=0, input=base, offset=0),
+        dict(weights=wg[0], flags=ql.QLIN_SWIGLU, gamma=gammas[1], eps=1e-6, input=base + 1, offset=0),
+        dict(weights=wd[0], flags=0, input=base + 2, offset=0),
+    ]
+    return stages, [wq, wo, wg, wd]
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_chain_qwen_layer(ws, rows):
+    gam = [synth.gamma(synth.HIDDEN, seed=910).to(DEV), synth.gamma(synth.HIDDEN, seed=911).to(DEV)]
+    stages, host = qwen_layer_stages(0, gam)
+    chain = ql.Chain(stages, max_rows=rows)
+    x = synth.activations(rows, synth.HIDDEN, seed=912, device=DEV)
+    y = chain.run(x)
+    torch.cuda.synchronize()
+    assert chain.status() == 0
+    check_against_single(ws, chain, stages, x, y, rows)
+    chain.close()
+
+
+def test_chain_two_layers_repeat(ws):
+    """Eight stages; three launches in a row give identical results (the counters
+    reset themselves at the end of each launch)."""
+    gam = [synth.gamma(synth.HIDDEN, seed=920 + i).to(DEV) for i in range(4)]
+    s0, h0 = qwen_layer_stages(0, gam[:2])
+    s1, h1 = qwen_layer_stages(1, gam[2:])
+    stages = s0 + s1
+    chain = ql.Chain(stages, max_rows=1)
+    x = synth.activations(1, synth.HIDDEN, seed=925, device=DEV)
+    first = chain.run(x).clone()
+    torch.cuda.synchronize()
+    check_against_single(ws, chain, stages, x, first, 1)
+    for _ in range(2):
+        y = chain.run(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y, first)
+    assert chain.status() == 0
+    chain.close()
+
+
+def test_chain_graph_replay():
+    gam = [synth.gamma(synth.HIDDEN, seed=930).to(DEV), synth.gamma(synth.HIDDEN, seed=931).to(DEV)]
+    stages, host = qwen_layer_stages(0, gam)
+    chain = ql.Chain(stages, max_rows=4)
+    x = synth.activations(4, synth.HIDDEN, seed=932, device=DEV)
+    y = torch.empty((4, synth.HIDDEN), dtype=torch.float16, device=DEV)
+    chain.run(x, out=y)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        chain.run(x, out=y)
+    for rep in range(3):
+        y.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {rep}"
+        chain.run(x, out=y)  # eager launch between replays
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+    assert chain.status() == 0
+    chain.close()
+
+
+def test_chain_rejects_bad_stages():
+    w_a = linear(4, 256, 512, 940)[0]
+    w_b = linear(8, 512, 256, 941)[0]
+    w_c = linear(4, 256, 96, 942)[0]  # N % 64 != 0
+    cases = [
+        ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=0, offset=4)], QLIN_ERR_PARAM),  # offset % 8
+        ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=1, offset=0)], QLIN_ERR_PARAM),  # not earlier
+        ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=0, offset=8)], QLIN_ERR_PARAM),  # past the end
+        ([dict(weights=w_c, flags=ql.QLIN_SWIGLU, input=-1, offset=0)], QLIN_ERR_UNSUPPORTED),
+        ([dict(weights=w_a, input=0, offset=0)], QLIN_ERR_PARAM),  # stage 0 must read the input
+    ]
+    for stages, rc in cases:
+        with pytest.raises(QlinError) as e:
+            ql.Chain(stages, max_rows=1)
+        assert e.value.rc == rc
+    with pytest.raises(QlinError):
+        ql.Chain([dict(weights=w_a, input=-1, offset=0)], max_rows=5)
+    chain = ql.Chain([dict(weights=w_a, input=-1, offset=0)], max_rows=2)
+    with pytest.raises(QlinError):
+        chain.run(torch.zeros((3, 256), dtype=torch.float16, device=DEV))  # rows > max_rows
+    chain.close()
+
+
+def test_chain_nonfinite_status():
+    w = linear(4, 256, 512, 950)[0]
+    chain = ql.Chain([dict(weights=w, input=-1, offset=0)], max_rows=1)
+    x = synth.activations(1, 256, seed=951, device=DEV)
+    x[0, 7] = float("inf")
+    chain.run(x)
+    assert chain.status(clear=True) == QLIN_ERR_NONFINITE
+    assert chain.status() == 0
+    chain.close()
