@@ -10,8 +10,11 @@ quantizes its fp16 input row itself.  The steps rotate over 36 distinct layer co
 Bytes per step = packed codes + f32 scales = 50,585,600.
 
 Also reported: the dominant kernel's roofline (the gate_up GEMV, HIP events on the
-launch stream), int8 TOPS of the M=512 prefill GEMMs of the same layer, and the
-CPU oracle timed on the host cores over a bounded sample of the same workload.
+launch stream), int8 TOPS of the M=512 prefill GEMMs of the same layer, the 36-layer
+mixed W4/W8 stack at M=1 and M=4 (RMSNorm before qkv and gate_up, one launch per
+linear and the one-launch decode chain), the M=4096 prefill layer with RMSNorm fused
+into the quantization of qkv and gate_up (Student-t activations), and the CPU oracle
+timed on the host cores over a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--prefill-reps R]
     python bench.py --mode kernel   # only the dominant kernel, for rocprofv3 --pmc passes
@@ -60,6 +63,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--mode", choices=["full", "kernel", "copy"], default="full")
+    ap.add_argument("--stack-reps", type=int, default=5)
+    ap.add_argument("--long-reps", type=int, default=3)
+    ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--no-long", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded "
@@ -212,6 +219,107 @@ def main():
         del g
     prefill_tops = tot_ops / (tot_us * 1e-6) / 1e12
 
+    # ---------------------------------------------------------------- 36-layer mixed stack
+    # qkv and gate_up W4 (the resident layers above), o and down W8; RMSNorm (eps 1e-6)
+    # before qkv and gate_up; o reads the q columns of qkv; fp16 between linears,
+    # requantized per token at every input.  Two executions of the same computation:
+    # one launch per linear (144 launches in one graph) and the decode chain (one
+    # persistent launch).
+    stack = None
+    if L >= 1 and not args.no_stack:
+        t0 = time.time()
+        w8 = []
+        for l in range(L):
+            pair = []
+            for p in (1, 3):
+                name, K, N = synth.LAYER[p]
+                packed, codes, sc = synth.make_linear(N, K, 8, synth.linear_seed(l, p, workload=4), device=dev,
+                                                      stack=True)
+                pair.append(ql.Weights.from_packed_device(8, K, N, packed, sc))
+                del packed, codes, sc
+            w8.append(pair)
+        gam = [(synth.gamma(synth.HIDDEN, seed=40000 + 2 * l, device=dev),
+                synth.gamma(synth.HIDDEN, seed=40001 + 2 * l, device=dev)) for l in range(L)]
+        torch.cuda.synchronize()
+        log(f"{L} layers of W8 o/down resident ({time.time() - t0:.1f} s)")
+        stack_bytes = sum(N * K // 2 + N * 4 for n, K, N in synth.LAYER if n in ("qkv", "gate_up")) + \
+            sum(N * K + N * 4 for n, K, N in synth.LAYER if n in ("o", "down"))
+        stack_bytes *= L
+        stack = {"bytes_per_step": stack_bytes, "layers": L}
+        for M in (1, 4):
+            x = synth.activations(M, synth.HIDDEN, seed=40100 + M, device=dev)
+            mids = [torch.empty((M, N // 2 if n == "gate_up" else N), dtype=torch.float16, device=dev)
+                    for n, K, N in synth.LAYER]
+            hs = [torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev) for _ in range(2)]
+
+            def stack_step(_i, M=M, x=x, mids=mids, hs=hs):
+                h = x
+                for l in range(L):
+                    ql.run(ws, layers[l][0], h, out=mids[0], gamma=gam[l][0], eps=1e-6)
+                    ql.run(ws, w8[l][0], mids[0][:, :4096], out=mids[1])
+                    ql.run(ws, layers[l][2], mids[1], out=mids[2], flags=ql.QLIN_SWIGLU, gamma=gam[l][1], eps=1e-6)
+                    h = hs[l % 2]
+                    ql.run(ws, w8[l][1], mids[2], out=h)
+
+            g = capture(stack_step, 1)
+            sec = time_graph(g, max(1, args.stack_reps))
+            us_l = sec * 1e6 / max(1, args.stack_reps)
+            del g
+            stages = []
+            for l in range(L):
+                b = 4 * l
+                stages += [dict(weights=layers[l][0], gamma=gam[l][0], eps=1e-6, input=b - 1 if l else -1),
+                           dict(weights=w8[l][0], input=b, offset=0),
+                           dict(weights=layers[l][2], flags=ql.QLIN_SWIGLU, gamma=gam[l][1], eps=1e-6, input=b + 1),
+                           dict(weights=w8[l][1], input=b + 2)]
+            chain = ql.Chain(stages, max_rows=M)
+            yc = torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev)
+            g = capture(lambda _i: chain.run(x, out=yc), 1)
+            sec = time_graph(g, max(1, args.stack_reps))
+            us_c = sec * 1e6 / max(1, args.stack_reps)
+            del g
+            ok = chain.status() == 0
+            same = bool(torch.equal(yc, hs[(L - 1) % 2]))
+            chain.close()
+            stack[f"m{M}"] = {
+                "launches_us": round(us_l, 1), "launches_gbs": round(stack_bytes / (us_l * 1e-6) / 1e9, 1),
+                "chain_us": round(us_c, 1), "chain_gbs": round(stack_bytes / (us_c * 1e-6) / 1e9, 1),
+                "chain_equals_launches": same and ok,
+            }
+            log(f"  stack {L} layers M={M}: launches {us_l:.0f} us ({stack[f'm{M}']['launches_gbs']} GB/s), "
+                f"chain {us_c:.0f} us ({stack[f'm{M}']['chain_gbs']} GB/s), outputs equal: {same and ok}")
+
+    # ---------------------------------------------------------------- prefill M=4096, fused RMSNorm
+    long_prefill = None
+    if not args.no_long:
+        M = 4096
+        ws_l = ql.Workspace(M, 9728, 19456)
+        g0 = synth.gamma(synth.HIDDEN, seed=50000, device=dev)
+        g1 = synth.gamma(synth.HIDDEN, seed=50001, device=dev)
+        la = [synth.activations(M, K, seed=50100 + p, device=dev, dist="student_t3")
+              for p, (_, K, _) in enumerate(synth.LAYER)]
+        lo = [torch.empty((M, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+              for name, K, N in synth.LAYER]
+        gam_l = [g0, None, g1, None]
+        per = {}
+        tot_ops, tot_us = 0.0, 0.0
+        for p, (name, K, N) in enumerate(synth.LAYER):
+            g = capture(lambda i, p=p: ql.run(ws_l, layers[i % L][p], la[p], out=lo[p], flags=flags[p],
+                                              gamma=gam_l[p], eps=1e-6), min(L, 8))
+            r = max(1, args.long_reps)
+            us = time_graph(g, r) * 1e6 / (r * min(L, 8))
+            ops = 2.0 * M * N * K
+            tot_ops += ops
+            tot_us += us
+            per[name] = {"us": round(us, 1), "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+            log(f"  prefill M=4096 {name}: {us:.1f} us, {per[name]['tops']} TOPS"
+                f"{' (RMSNorm + quant + GEMM)' if gam_l[p] is not None else ' (quant + GEMM)'}")
+            del g
+        long_prefill = {"tops": round(tot_ops / (tot_us * 1e-6) / 1e12, 1),
+                        "frac_of_int8_peak": round(tot_ops / (tot_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+                        "us_per_layer": round(tot_us, 1), "per_proj": per}
+        ws_l.close()
+
     # ---------------------------------------------------------------- CPU oracle baseline
     cpu = None
     if not args.no_cpu:
@@ -268,6 +376,8 @@ def main():
         "per_kernel_decode": per_kernel,
         "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
                          "per_proj": prefill},
+        "decode_stack_mixed": stack,
+        "prefill_m4096_rmsnorm": long_prefill,
     }
     print(json.dumps(result), flush=True)
 

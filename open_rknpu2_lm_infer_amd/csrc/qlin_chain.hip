@@ -134,37 +134,12 @@ __device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const
     if (st.gamma) {
         if (wave < M) {
             const __half* xr = lds_x + wave * K;
-            if (st.flags & kFlagNormSeq) {
-                if (lane == 0) {  // src/ops/norm.rs:38
-                    float sum = 0.0f;
-                    for (int i = 0; i < K; ++i) {
-                        const float v = __half2float(xr[i]);
-                        const float v2 = v * v;
-                        sum = sum + v2;
-                    }
-                    s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
-                }
-            } else {  // src/model/cpu.rs:14-35, 16 FMA chains
-                const int j = lane & 15;
-                float acc = 0.0f;
-                if (lane < 16)
-                    for (int i = 0; i + 16 <= K; i += 16) {
-                        const float v = __half2float(xr[i + j]);
-                        acc = __builtin_fmaf(v, v, acc);
-                    }
-                const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
-                const float tj = (acc + b) + (c + d);
-                const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
-                if (lane == 0) {
-                    float sum = (tj + t1) + (t2 + t3);
-                    for (int i = K & ~15; i < K; ++i) {
-                        const float v = __half2float(xr[i]);
-                        const float v2 = v * v;
-                        sum = sum + v2;
-                    }
-                    s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
-                }
-            }
+            float sum;
+            if (st.flags & kFlagNormSeq)
+                sum = lane == 0 ? lds_sumsq_seq(xr, K) : 0.0f;  // src/ops/norm.rs:38
+            else
+                sum = lds_sumsq_neon16(xr, K);  // src/model/cpu.rs:14-35
+            if (lane == 0) s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
         }
         __syncthreads();
     }

@@ -255,31 +255,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                 }
             }
             __syncthreads();
-            if ((p.flags & kFlagNormSeq) != 0) {
-                if (tid == 0) {  // src/ops/norm.rs:38
-                    float sum = 0.0f;
-                    for (int i = 0; i < p.K; ++i) {
-                        const float v2 = lds_x[i] * lds_x[i];
-                        sum = sum + v2;
-                    }
-                    s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
-                }
-            } else if (tid < 64) {  // src/model/cpu.rs:14-35, 16 FMA chains
-                const int j = tid & 15;
-                float acc = 0.0f;
-                if (tid < 16)
-                    for (int i = 0; i + 16 <= p.K; i += 16) acc = __builtin_fmaf(lds_x[i + j], lds_x[i + j], acc);
-                const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
-                const float tj = (acc + b) + (c + d);
-                const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
-                if (tid == 0) {
-                    float sum = (tj + t1) + (t2 + t3);
-                    for (int i = p.K & ~15; i < p.K; ++i) {
-                        const float v2 = lds_x[i] * lds_x[i];
-                        sum = sum + v2;
-                    }
-                    s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
-                }
+            if (tid < 64) {
+                const float sum = (p.flags & kFlagNormSeq) != 0 ? (tid == 0 ? lds_sumsq_seq(lds_x, p.K) : 0.0f)  // src/ops/norm.rs:38
+                                                                : lds_sumsq_neon16(lds_x, p.K);  // src/model/cpu.rs:14-35
+                if (tid == 0) s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
             }
             __syncthreads();
             nscale = s_inv[0];

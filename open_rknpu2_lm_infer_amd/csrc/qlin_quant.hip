@@ -110,39 +110,11 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_staged_kernel(QuantPar
 
     float nscale = 1.0f;
     if (p.gamma) {
-        // RMSNorm scale with the reference's summation order (see block_rms_scale)
-        if (p.flags & kFlagNormSeq) {
-            if (t == 0) {
-                float sum = 0.0f;
-                for (int i = 0; i < p.K; ++i) {
-                    const float v = lds_ld(xs, i);
-                    const float v2 = v * v;
-                    sum = sum + v2;
-                }
-                red[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
-            }
-        } else if (t < 64) {
-            float acc = 0.0f;
-            const int j = t & 15;
-            if (t < 16) {
-                const int n16 = p.K & ~15;
-                for (int i = 0; i < n16; i += 16) {
-                    const float v = lds_ld(xs, i + j);
-                    acc = __builtin_fmaf(v, v, acc);
-                }
-            }
-            const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
-            const float tj = (acc + b) + (c + d);
-            const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
-            if (t == 0) {
-                float sum = (tj + t1) + (t2 + t3);
-                for (int i = p.K & ~15; i < p.K; ++i) {
-                    const float v = lds_ld(xs, i);
-                    const float v2 = v * v;
-                    sum = sum + v2;
-                }
-                red[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
-            }
+        // RMSNorm scale with the reference's summation order (wave 0)
+        if (t < 64) {
+            const float sum = (p.flags & kFlagNormSeq) ? (t == 0 ? lds_sumsq_seq(xs, p.K) : 0.0f)
+                                                       : lds_sumsq_neon16(xs, p.K);
+            if (t == 0) red[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
         }
         __syncthreads();
         nscale = red[0];

@@ -121,6 +121,74 @@ __device__ float block_rms_scale(const T* row, int K, float eps, bool sequential
     return r;
 }
 
+template <typename T>
+__device__ __forceinline__ float lds_f32(const T* p, int i) {
+    if constexpr (sizeof(T) == 2) return __half2float(p[i]);
+    else return p[i];
+}
+
+// Sum of squares of a row held in LDS, in the order of src/ops/norm.rs:38
+// (sum = sum + v*v, one rounding per operation).  One thread.  The loads of 16
+// elements are issued before their additions, so LDS latency is paid once per 16.
+template <typename T>
+__device__ float lds_sumsq_seq(const T* x, int K) {
+    float sum = 0.0f;
+    int i = 0;
+    for (; i + 16 <= K; i += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = lds_f32(x, i + u);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float v2 = v[u] * v[u];
+            sum = sum + v2;
+        }
+    }
+    for (; i < K; ++i) {
+        const float v = lds_f32(x, i);
+        const float v2 = v * v;
+        sum = sum + v2;
+    }
+    return sum;
+}
+
+// Sum of squares of a row held in LDS, in the order of src/model/cpu.rs:14-35: 16
+// fused-multiply-add chains (chain j takes elements j, j+16, ... in order), combined
+// lanewise as (a+b)+(c+d), then (t0+t1)+(t2+t3), then the scalar tail sum += v*v.
+// Called by all 64 lanes of one wave; the result is valid in lane 0.  Each chain
+// issues the loads of 16 elements before their FMAs.
+template <typename T>
+__device__ float lds_sumsq_neon16(const T* x, int K) {
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    float acc = 0.0f;
+    if (lane < 16) {
+        const int n16 = K & ~15;
+        int i = 0;
+        for (; i + 256 <= n16; i += 256) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = lds_f32(x, i + 16 * u + j);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(v[u], v[u], acc);
+        }
+        for (; i < n16; i += 16) {
+            const float v = lds_f32(x, i + j);
+            acc = __builtin_fmaf(v, v, acc);
+        }
+    }
+    const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
+    const float tj = (acc + b) + (c + d);
+    const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
+    float sum = (tj + t1) + (t2 + t3);
+    if (lane == 0)
+        for (int i = K & ~15; i < K; ++i) {
+            const float v = lds_f32(x, i);
+            const float v2 = v * v;
+            sum = sum + v2;
+        }
+    return sum;
+}
+
 // Block-wide max of non-negative values and OR of flags.  lds: >= 8 words.
 __device__ __forceinline__ void block_max_or(float& v, int& f, float* lds) {
     v = wave_max(v);
