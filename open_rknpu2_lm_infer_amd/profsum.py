@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 result databases (SQLite, the default rocprofv3 output).
 
-    python -m open_rknpu2_lm_infer_amd.profsum stats  RESULTS.db [--match REGEX]
+    python -m open_rknpu2_lm_infer_amd.profsum stats  RESULTS.db [--match REGEX] [--md]
     python -m open_rknpu2_lm_infer_amd.profsum pmc    RESULTS.db [--match REGEX]
     python -m open_rknpu2_lm_infer_amd.profsum traffic --fetch F.db --write W.db \
         --copy-fetch CF.db --copy-write CW.db --copy-bytes B --match REGEX
@@ -71,7 +71,18 @@ def main(argv=None):
     ap.add_argument("--copy-write")
     ap.add_argument("--copy-match", default="copyBuffer")
     ap.add_argument("--copy-bytes", type=float)
+    ap.add_argument("--md", action="store_true", help="stats as a markdown table with each kernel's share")
     a = ap.parse_args(argv)
+    if a.what == "stats" and a.md:
+        rows = kernel_stats(a.db, a.match)
+        total = sum(r["avg_us"] * r["dispatches"] for r in rows) or 1.0
+        print("| kernel | grid (workgroups x size) | calls | avg us | min us | max us | share of listed time |")
+        print("|---|---|---:|---:|---:|---:|---:|")
+        for r in rows:
+            share = 100.0 * r["avg_us"] * r["dispatches"] / total
+            print(f"| `{r['name'][:100]}` | {r['workgroups']}x{r['wg_size']} | {r['dispatches']} | {r['avg_us']:.2f} | "
+                  f"{r['min_us']:.2f} | {r['max_us']:.2f} | {share:.1f}% |")
+        return 0
     if a.what == "stats":
         for r in kernel_stats(a.db, a.match):
             print(f"{r['avg_us']:9.2f} us avg  {r['min_us']:8.2f} min  {r['max_us']:8.2f} max  n={r['dispatches']:6d}  "
