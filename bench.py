@@ -67,6 +67,8 @@ def main():
     ap.add_argument("--long-reps", type=int, default=3)
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--no-long", action="store_true")
+    ap.add_argument("--no-head", action="store_true")
+    ap.add_argument("--head-reps", type=int, default=25)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded "
@@ -218,6 +220,28 @@ def main():
         log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM)")
         del g
     prefill_tops = tot_ops / (tot_us * 1e-6) / 1e12
+
+    # ---------------------------------------------------------------- W8 lm_head at M=1
+    # 151,936 x 2560 int8 (389 MB, larger than the Infinity Cache): one GEMV launch.
+    head = None
+    if not args.no_head:
+        Kh, Nh = synth.HIDDEN, 151936
+        packed, codes, sc = synth.make_linear(Nh, Kh, 8, synth.linear_seed(0, 0, workload=6), device=dev)
+        w_head = ql.Weights.from_packed_device(8, Kh, Nh, packed, sc)
+        del packed, codes, sc
+        xh = synth.activations(1, Kh, seed=60001, device=dev)
+        yh = torch.empty((1, Nh), dtype=torch.float16, device=dev)
+        ws_head = ql.Workspace(1, Kh, Nh)
+        g = capture(lambda i: ql.run(ws_head, w_head, xh, out=yh), 4)
+        r = max(1, args.head_reps)
+        us = time_graph(g, r) * 1e6 / (r * 4)
+        hb = Nh * Kh + Nh * 4
+        head = {"us": round(us, 2), "bytes": hb, "gbs": round(hb / (us * 1e-6) / 1e9, 1),
+                "frac_of_hbm": round(hb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"  lm_head W8 151936x2560 M=1: {us:.1f} us, {head['gbs']} GB/s")
+        del g
+        w_head.close()
+        ws_head.close()
 
     # ---------------------------------------------------------------- 36-layer mixed stack
     # qkv and gate_up W4 (the resident layers above), o and down W8; RMSNorm (eps 1e-6)
@@ -376,6 +400,7 @@ def main():
         "per_kernel_decode": per_kernel,
         "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
                          "per_proj": prefill},
+        "lm_head_w8_m1": head,
         "decode_stack_mixed": stack,
         "prefill_m4096_rmsnorm": long_prefill,
     }

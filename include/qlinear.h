@@ -64,7 +64,7 @@ typedef struct qlin_weight_config {
 /* Reference: rk_npu_w4a8_weight_info / rk_npu_i4_weights_memory_query (src/npu.rs:408-423). */
 typedef struct qlin_weight_info {
     int32_t bits, K, N;
-    int32_t K_padded;      /* K rounded up to 128 (zero codes in the pad) */
+    int32_t K_padded;      /* K rounded up to 256 (zero codes in the pad) */
     int32_t N_padded;      /* N rounded up to 64 (zero codes and scales in the pad) */
     int32_t device;        /* HIP device ordinal holding the weights */
     uint64_t device_bytes; /* packed codes + scales resident in HBM */
@@ -110,6 +110,21 @@ int qlin_weights_create_packed(const qlin_weight_config* config, const void* pac
  * (copied device-to-device on `stream`); no host round trip for large stacks. */
 int qlin_weights_create_packed_device(const qlin_weight_config* config, const void* packed_nk,
                                       const float* scales, void* stream, qlin_weights** out);
+
+/* compressed-tensors storage straight to the device layout.  Replaces QuantLoader::load's
+ * unpack + [K,N] transpose (src/model/checkpoint.rs:320-390) and concatenate along N
+ * (src/model/checkpoint.rs:392-423) for the engine's fused projections.
+ * QLIN_PACK_QUANTIZED: data[i] is the I32 tensor weight_packed [part_n[i], ceil(K*bits/32)], fields
+ *   LSB-first, code = field - 2^(bits-1) (checkpoint.rs:352-371).
+ * QLIN_INT_QUANTIZED (bits = 8 only): data[i] is the I8 tensor weight [part_n[i], K] (checkpoint.rs:372-378).
+ * The parts are stacked along N in order (q, k, v or gate, up); config->N = sum of part_n.  data and
+ * scales are host pointers (e.g. the mmap'd tensors); scales[i] is f32 [part_n[i]], positive and finite.
+ * Like the reference loader, code values are not range-checked (a W8 field 0 decodes to -128). */
+#define QLIN_PACK_QUANTIZED 0
+#define QLIN_INT_QUANTIZED 1
+int qlin_weights_create_compressed(const qlin_weight_config* config, int32_t format, int32_t n_parts,
+                                   const int32_t* part_n, const void* const* data,
+                                   const float* const* scales, qlin_weights** out);
 
 /* Replaces rk_npu_w4a8_weights_free / rk_npu_f32i8f32_weights_free (src/npu.rs:411,452). */
 void qlin_weights_free(qlin_weights* weights);
@@ -182,6 +197,23 @@ int qlin_gemm_i32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
 int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
                        const int8_t* q, int64_t ldq, const float* s, void* C, int32_t c_dtype,
                        int64_t ldc, uint32_t flags, void* stream);
+
+/* ---- kernel-variant selection ----
+ * Replaces the NPU strategy search and its on-disk cache (src/npu.rs:595-996, driven by
+ * src/cli/tune.rs:10-59).  qlin_tune times, on `stream`, the variants of the path a run of
+ * `rows` rows takes (decode GEMV: 4, 8 or 16 waves per channel group; GEMM: 1..8 k splits),
+ * checks that they all produce the same output, and records the fastest for the key (bits,
+ * K, N, rows bucket, path, QLIN_SWIGLU); later runs with that key use it.  The table is
+ * process-wide (all devices; tune on the device that runs).  QLIN_GEMV_WAVES and
+ * QLIN_GEMM_SPLITS in the environment still take precedence.  flags: 0 or QLIN_SWIGLU.
+ * qlin_tune_load returns the number of entries read (or an error code); the file is text,
+ * one entry per line. */
+int qlin_tune(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, uint32_t flags, int32_t reps,
+              void* stream);
+int qlin_tune_count(void);
+void qlin_tune_clear(void);
+int qlin_tune_save(const char* path);
+int qlin_tune_load(const char* path);
 
 /* ---- decode chain: several linears in one launch (1..4 rows, fp16 activations) ----
  * Replaces the per-projection calls of the decode step, src/model/dense.rs:398-540

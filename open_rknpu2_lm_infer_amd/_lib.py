@@ -29,6 +29,9 @@ QLIN_NORM_SEQUENTIAL = 0x2
 QLIN_SWIGLU = 0x4
 QLIN_NO_FUSED_QUANT = 0x8
 
+QLIN_PACK_QUANTIZED = 0
+QLIN_INT_QUANTIZED = 1
+
 # Every function declared in include/qlinear.h: name -> (restype, argtypes)
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -54,6 +57,12 @@ SIGNATURES = {
     "qlin_quantize": (ctypes.c_int, [_I32, _I32, _P, _I32, _I64, _P, _F, _P, _I64, _P, _P, _U32, _P]),
     "qlin_gemm_i32": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _I64, _P]),
     "qlin_run_quantized": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _P, _I32, _I64, _U32, _P]),
+    "qlin_weights_create_compressed": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _P]),
+    "qlin_tune": (ctypes.c_int, [_P, _P, _I32, _U32, _I32, _P]),
+    "qlin_tune_count": (ctypes.c_int, []),
+    "qlin_tune_clear": (None, []),
+    "qlin_tune_save": (ctypes.c_int, [ctypes.c_char_p]),
+    "qlin_tune_load": (ctypes.c_int, [ctypes.c_char_p]),
     "qlin_chain_create": (ctypes.c_int, [_P, _I32, _I32, _P]),
     "qlin_chain_free": (None, [_P]),
     "qlin_chain_run": (ctypes.c_int, [_P, _I32, _P, _I64, _P, _I64, _P]),

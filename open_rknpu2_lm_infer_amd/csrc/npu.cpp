@@ -3,6 +3,7 @@
 #include "npu.hpp"
 
 #include <algorithm>
+#include <cstdio>
 #include <sstream>
 
 #include "../../include/qlinear.h"
@@ -45,6 +46,9 @@ struct Workspace {
 struct Backend::Inner {
     ModelOptions options;
     uint32_t domain_id = 0;
+    std::vector<std::weak_ptr<Weights>> linears;  // live weights, for the variant search
+    std::vector<std::pair<const Weights*, size_t>> searched;  // (weights, bucket) already searched
+    size_t tune_calls = 0;
     std::map<size_t, std::unique_ptr<Workspace>> work;  // bucket rows -> workspace
     int max_k = 0, max_n = 0;                           // largest loaded geometry
     size_t loaded_w4 = 0, loaded_w8 = 0, geometries = 0;
@@ -65,7 +69,7 @@ struct Backend::Inner {
 
 struct Linear::State {
     std::shared_ptr<Backend::Inner> owner;  // a Linear keeps its Backend alive (src/npu.rs:255-260)
-    std::unique_ptr<Weights> weights;
+    std::shared_ptr<Weights> weights;
     uint32_t bits = 0;
     size_t k = 0, n = 0;
 };
@@ -77,6 +81,14 @@ Backend Backend::create(const ModelOptions& options, uint32_t domain_id) {
     b.inner = std::make_shared<Inner>();
     b.inner->options = options;
     b.inner->domain_id = domain_id;
+    if (!options.tune_cache.empty()) {
+        // src/npu.rs:665-680: a missing cache file is not an error
+        if (std::FILE* f = std::fopen(options.tune_cache.c_str(), "r")) {
+            std::fclose(f);
+            const int n = qlin_tune_load(options.tune_cache.c_str());
+            check(n < 0 ? n : QLIN_OK, "load tune cache");
+        }
+    }
     return b;
 }
 
@@ -93,7 +105,7 @@ Linear Backend::load(QuantMatrix matrix) {
     lin.state->bits = matrix.bits;
     lin.state->k = matrix.k;
     lin.state->n = matrix.n;
-    lin.state->weights = std::make_unique<Weights>();
+    lin.state->weights = std::make_shared<Weights>();
     qlin_weight_config cfg{(int32_t)matrix.bits, (int32_t)matrix.k, (int32_t)matrix.n};
     check(qlin_weights_create(&cfg, matrix.codes.data(), matrix.scales.data(), &lin.state->weights->raw),
           matrix.bits == 4 ? "W4 weights" : "W8 weights");
@@ -105,12 +117,35 @@ Linear Backend::load(QuantMatrix matrix) {
     inner->max_k = std::max(inner->max_k, (int)matrix.k);
     inner->max_n = std::max(inner->max_n, (int)matrix.n);
     inner->get_work(1);
+    inner->linears.push_back(lin.state->weights);
     matrix.codes.clear();  // the device copy is the only one kept (src/npu.rs:459-477)
     matrix.codes.shrink_to_fit();
     return lin;
 }
 
-void Backend::prepare(size_t rows) { inner->get_work(bucket(rows)); }
+void Backend::prepare(size_t rows) {
+    const size_t m = bucket(rows);
+    Workspace* ws = inner->get_work(m);
+    if (!inner->options.tune_search) return;
+    size_t before = inner->tune_calls;
+    for (auto& weak : inner->linears) {
+        auto w = weak.lock();
+        if (!w) continue;
+        const std::pair<const Weights*, size_t> key{w.get(), m};
+        if (std::find(inner->searched.begin(), inner->searched.end(), key) != inner->searched.end()) continue;
+        qlin_weight_info info{};
+        check(qlin_weights_query(w->raw, &info), "weight query");
+        check(qlin_tune(ws->raw, w->raw, (int32_t)m, 0, 20, nullptr), "tune");
+        ++inner->tune_calls;
+        if (info.N % 64 == 0) {
+            check(qlin_tune(ws->raw, w->raw, (int32_t)m, QLIN_SWIGLU, 20, nullptr), "tune");
+            ++inner->tune_calls;
+        }
+        inner->searched.push_back(key);
+    }
+    if (inner->tune_calls != before && !inner->options.tune_cache.empty())
+        check(qlin_tune_save(inner->options.tune_cache.c_str()), "save tune cache");
+}
 
 void Backend::retain_workspaces(const std::vector<size_t>& rows) {
     std::vector<size_t> keep;
@@ -125,7 +160,7 @@ void Backend::retain_workspaces(const std::vector<size_t>& rows) {
 
 uint64_t Backend::weight_bytes() const { return inner->weight_bytes; }
 
-size_t Backend::tune_operations() const { return 0; }
+size_t Backend::tune_operations() const { return inner->tune_calls; }
 
 std::string Backend::stats() const {
     uint64_t ws_bytes = 0;
@@ -137,7 +172,7 @@ std::string Backend::stats() const {
     o << "{\"backend\": \"qlinear-gfx950\", \"loaded_w4\": " << inner->loaded_w4
       << ", \"loaded_w8\": " << inner->loaded_w8 << ", \"weight_payload_bytes\": " << inner->weight_bytes
       << ", \"workspace_payload_bytes\": " << ws_bytes << ", \"workspace_count\": " << inner->work.size()
-      << ", \"tune_cache_hits\": 0, \"tune_cache_misses\": 0, \"tune_calls\": 0"
+      << ", \"tune_calls\": " << inner->tune_calls << ", \"tune_entries\": " << qlin_tune_count()
       << ", \"strategy_fallbacks\": 0, \"strategy_fallback_calls\": 0, \"weight_reload_calls\": 0"
       << ", \"weight_geometries\": " << inner->geometries << ", \"device\": " << inner->options.device
       << ", \"domain_id\": " << inner->domain_id << "}";

@@ -33,7 +33,9 @@ struct Error : std::runtime_error {
 struct ModelOptions {
     size_t chunk = 128;   // ubatch rows, 1..256 (src/npu.rs:52-55)
     int device = 0;       // HIP device of this backend (the reference's NPU domain)
-    bool tune = false;    // accepted for parity; kernels are selected per shape, no search
+    bool tune = false;         // heuristic variant choice, no search (the reference's `tune`)
+    bool tune_search = false;  // prepare() times the kernel variants of every live linear (src/npu.rs:728-940)
+    std::string tune_cache;    // variant table file: read by create(), written after a search (src/npu.rs:665-680)
 };
 
 // src/npu.rs:112-118: codes int8 [K, N] K-major (codes[k*N + n]), scales f32 [N].
@@ -56,12 +58,15 @@ public:
     // src/npu.rs:368-484: validates bits/dims/lengths, copies the codes to HBM, and
     // prepares the one-row workspace.  The host codes are released on return.
     Linear load(QuantMatrix matrix);
-    // src/npu.rs:595-615: workspaces for bucket(rows) of every loaded geometry.
+    // src/npu.rs:595-615: workspaces for bucket(rows) of every loaded geometry; with
+    // options.tune_search, also the variant search (qlin_tune) for bucket(rows) of every live
+    // linear not searched yet (plain and, where N % 64 == 0, SwiGLU), saved to
+    // options.tune_cache when set.
     void prepare(size_t rows);
     // src/npu.rs:616-623: drops workspaces whose bucket is not in `rows`.
     void retain_workspaces(const std::vector<size_t>& rows);
     uint64_t weight_bytes() const;
-    size_t tune_operations() const;  // strategy cache lookups: none on this path
+    size_t tune_operations() const;  // variant searches run (src/npu.rs:627)
     std::string stats() const;       // JSON, src/npu.rs:631-661
 
     struct Inner;

@@ -5,9 +5,13 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <new>
+#include <tuple>
 #include <vector>
 
 #include "../../include/qlinear.h"
@@ -52,10 +56,63 @@ int env_int(const char* name, int dflt) {
 
 int current_device(int* dev) { return hipGetDevice(dev) == hipSuccess ? QLIN_OK : QLIN_ERR_NODEVICE; }
 
+// ---- kernel-variant table (qlin_tune) ------------------------------------------------
+// Key: bits, K, N, rows bucket, path (0 decode GEMV with fused quantization, 1 decode GEMV
+// from quantized rows, 2 GEMM), SwiGLU.  Value: GEMV waves per group or GEMM k splits.
+using TuneKey = std::tuple<int, int, int, int, int, int>;
+std::map<TuneKey, int>& tune_table() {
+    static std::map<TuneKey, int> t;
+    return t;
+}
+std::mutex& tune_mutex() {
+    static std::mutex m;
+    return m;
+}
+thread_local int g_force_variant = 0;  // set by qlin_tune while it times one candidate
+
+int rows_bucket(int rows) {
+    if (rows <= kGemvMaxRows) return rows;
+    int b = 32;
+    while (b < rows && b < 4096) b *= 2;
+    return rows <= 4096 ? b : (rows + 1023) / 1024 * 1024;
+}
+
+int tuned_variant(int bits, int K, int N, int rows, int path, bool sw) {
+    if (g_force_variant) return g_force_variant;
+    std::lock_guard<std::mutex> g(tune_mutex());
+    auto it = tune_table().find(TuneKey{bits, K, N, rows_bucket(rows), path, sw ? 1 : 0});
+    return it == tune_table().end() ? 0 : it->second;
+}
+
+
+
 int cu_count(int dev) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     return n;
+}
+
+// compressed-tensors rows -> device rows.  W4 pack-quantized: the words' little-endian bytes
+// hold codes 2j (low nibble) and 2j+1 as field = code + 8, whose two's-complement nibble is
+// field ^ 8; W8 pack-quantized: byte ^ 0x80; W8 int-quantized: the byte itself.  Codes at
+// k >= K and bytes past the row become zero.
+__global__ void unpack_compressed_kernel(const uint8_t* src, int64_t src_row, int rows, int bits, int fmt, int K,
+                                         uint8_t* dst, int64_t wrow) {
+    const int64_t total = (int64_t)rows * wrow;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / wrow, j = i - r * wrow;
+        uint8_t out = 0;
+        if (bits == 4) {
+            if (2 * j < K) {
+                const uint8_t b = src[r * src_row + j] ^ 0x88u;
+                out = (uint8_t)((b & 0x0Fu) | (2 * j + 1 < K ? (b & 0xF0u) : 0u));
+            }
+        } else if (j < K) {
+            const uint8_t b = src[r * src_row + j];
+            out = fmt == 0 ? (uint8_t)(b ^ 0x80u) : b;
+        }
+        dst[i] = out;
+    }
 }
 
 __global__ void pack_kn_kernel(const int8_t* codes, int K, int N, int Kp, int Np, int bits, uint8_t* out) {
@@ -224,6 +281,55 @@ static int create_packed(const qlin_weight_config* config, const void* packed, c
     return QLIN_OK;
 }
 
+int qlin_weights_create_compressed(const qlin_weight_config* config, int32_t format, int32_t n_parts,
+                                   const int32_t* part_n, const void* const* data, const float* const* scales,
+                                   qlin_weights** out) {
+    if (!out) return QLIN_ERR_PARAM;
+    *out = nullptr;
+    if (int rc = check_config(config)) return rc;
+    if ((format != QLIN_PACK_QUANTIZED && format != QLIN_INT_QUANTIZED) || n_parts < 1 || !part_n || !data ||
+        !scales || (format == QLIN_INT_QUANTIZED && config->bits != 8))
+        return QLIN_ERR_PARAM;
+    int64_t n_total = 0;
+    for (int i = 0; i < n_parts; ++i) {
+        if (part_n[i] <= 0 || !data[i]) return QLIN_ERR_PARAM;
+        if (int rc = check_scales(scales[i], part_n[i])) return rc;
+        n_total += part_n[i];
+    }
+    if (n_total != config->N) return QLIN_ERR_PARAM;
+    const int64_t factor = 32 / config->bits;
+    const int64_t src_row = format == QLIN_INT_QUANTIZED ? config->K : (config->K + factor - 1) / factor * 4;
+    qlin_weights* w = nullptr;
+    if (int rc = alloc_weights(config, &w)) return rc;
+    int max_part = 0;
+    for (int i = 0; i < n_parts; ++i) max_part = std::max(max_part, part_n[i]);
+    uint8_t* staging = nullptr;
+    int rc = QLIN_OK;
+    if (hipMalloc(&staging, (size_t)max_part * src_row) != hipSuccess) rc = QLIN_ERR_NOMEM;
+    if (!rc && (hipMemset(w->W, 0, (size_t)w->Np * w->wrow) != hipSuccess ||
+                hipMemset(w->scales, 0, (size_t)w->Np * sizeof(float)) != hipSuccess))
+        rc = QLIN_ERR_DEVICE;
+    int64_t row0 = 0;
+    for (int i = 0; i < n_parts && !rc; ++i) {
+        if (hipMemcpy(staging, data[i], (size_t)part_n[i] * src_row, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(w->scales + row0, scales[i], (size_t)part_n[i] * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            rc = QLIN_ERR_DEVICE;
+            break;
+        }
+        hipLaunchKernelGGL(unpack_compressed_kernel, dim3(1024), dim3(256), 0, nullptr, staging, src_row, part_n[i],
+                           config->bits, format, config->K, w->W + row0 * w->wrow, w->wrow);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = QLIN_ERR_DEVICE;
+        row0 += part_n[i];
+    }
+    (void)hipFree(staging);
+    if (rc) {
+        qlin_weights_free(w);
+        return rc;
+    }
+    *out = w;
+    return QLIN_OK;
+}
+
 int qlin_weights_create_packed(const qlin_weight_config* config, const void* packed_nk, const float* scales,
                                qlin_weights** out) {
     return create_packed(config, packed_nk, scales, hipMemcpyHostToDevice, nullptr, out);
@@ -381,7 +487,12 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
     const int groups = (sw ? w->N / 2 : w->Np) / 16;
     int waves = env_int("QLIN_GEMV_WAVES", 0);
-    if (waves != 4 && waves != 8 && waves != 16) waves = gemv_pick_waves(groups, steps);
+    if (waves != 4 && waves != 8 && waves != 16) {
+        waves = tuned_variant(w->bits, w->K, w->N, rows, A ? 0 : 1, sw);
+        // a tuned count must still let the fused prologue hold the rows in registers
+        if ((waves != 4 && waves != 8 && waves != 16) || (A && !gemv_can_fuse(rows, w->K, waves, gamma != nullptr)))
+            waves = gemv_pick_waves(groups, steps);
+    }
     return launch_gemv(p, w->bits, waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
@@ -425,6 +536,7 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     const int tiles = p.m_tiles * p.n_tiles;
     const int64_t slice = (int64_t)gemm_regs_per_thread(bn) * 256;  // ints of one partial tile
     int S = env_int("QLIN_GEMM_SPLITS", 0);
+    if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
     if (S <= 0) {
         // split K until the grid covers the CUs, keeping >= 4 k tiles per split
         // split-K's partial round trip costs more than a second resident workgroup
@@ -729,4 +841,110 @@ int qlin_chain_status(qlin_chain* c, int32_t clear) {
     if (clear && e && hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess) return QLIN_ERR_DEVICE;
     if (hipDeviceSynchronize() != hipSuccess) return QLIN_ERR_DEVICE;
     return (e & 2u) ? QLIN_ERR_DEVICE : (e ? QLIN_ERR_NONFINITE : QLIN_OK);
+}
+
+// ---- kernel-variant selection ---------------------------------------------------------
+
+int qlin_tune(qlin_workspace* ws, const qlin_weights* w, int32_t rows, uint32_t flags, int32_t reps, void* stream) {
+    if (!ws || !w || rows <= 0 || rows > ws->max_rows || reps < 1 || (flags & ~(uint32_t)QLIN_SWIGLU)) return QLIN_ERR_PARAM;
+    if (int rc = check_run(ws, w, rows, flags)) return rc;
+    const bool sw = (flags & kFlagSwiglu) != 0;
+    const int ncols = sw ? w->N / 2 : w->N;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    _Float16 *A = nullptr, *C = nullptr;
+    const size_t a_bytes = (size_t)rows * w->K * sizeof(_Float16), c_bytes = (size_t)rows * ncols * sizeof(_Float16);
+    if (hipMalloc(&A, a_bytes) != hipSuccess || hipMalloc(&C, c_bytes) != hipSuccess) {
+        (void)hipFree(A);
+        return QLIN_ERR_NOMEM;
+    }
+    int rc = hipMemset(A, 0x3c, a_bytes) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;  // every value 1.0 (0x3c3c)
+    const bool fused = gemv_fusable(w, rows, A, w->K, nullptr, flags);
+    const int path = fused ? 0 : (gemv_ok(ws, w, rows) ? 1 : 2);
+    std::vector<int> cand;
+    if (path < 2) {
+        for (int v : {4, 8, 16})
+            if (!fused || gemv_can_fuse(rows, w->K, v, false)) cand.push_back(v);
+    } else {
+        const int ktiles = w->Kp / kGemmTileK;
+        for (int v : {1, 2, 3, 4, 6, 8})
+            if (2 * v <= ktiles) cand.push_back(v);
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)) rc = QLIN_ERR_DEVICE;
+    std::vector<uint16_t> ref(c_bytes / 2), got(c_bytes / 2);
+    float best_ms = 0.0f;
+    int best = 0;
+    for (size_t i = 0; i < cand.size() && !rc; ++i) {
+        g_force_variant = cand[i];
+        rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);  // warm-up
+        if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = QLIN_ERR_DEVICE;
+        for (int r = 0; r < reps && !rc; ++r)
+            rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);
+        float ms = 0.0f;
+        if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                    hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+            rc = QLIN_ERR_DEVICE;
+        // every variant computes the same integers and epilogue: the outputs must agree
+        if (!rc && hipMemcpy((i == 0 ? ref : got).data(), C, c_bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = QLIN_ERR_DEVICE;
+        if (!rc && i > 0 && std::memcmp(ref.data(), got.data(), c_bytes) != 0) rc = QLIN_ERR_DEVICE;
+        if (!rc && (best == 0 || ms < best_ms)) {
+            best_ms = ms;
+            best = cand[i];
+        }
+    }
+    g_force_variant = 0;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(A);
+    (void)hipFree(C);
+    if (!rc && best) {
+        std::lock_guard<std::mutex> g(tune_mutex());
+        tune_table()[TuneKey{w->bits, w->K, w->N, rows_bucket(rows), path, sw ? 1 : 0}] = best;
+    }
+    return rc;
+}
+
+int qlin_tune_count(void) {
+    std::lock_guard<std::mutex> g(tune_mutex());
+    return (int)tune_table().size();
+}
+
+void qlin_tune_clear(void) {
+    std::lock_guard<std::mutex> g(tune_mutex());
+    tune_table().clear();
+}
+
+int qlin_tune_save(const char* path) {
+    if (!path) return QLIN_ERR_PARAM;
+    std::FILE* f = std::fopen(path, "w");
+    if (!f) return QLIN_ERR_PARAM;
+    std::lock_guard<std::mutex> g(tune_mutex());
+    std::fprintf(f, "# qlinear variant table: bits K N rows_bucket path swiglu variant\n");
+    for (auto& kv : tune_table())
+        std::fprintf(f, "%d %d %d %d %d %d %d\n", std::get<0>(kv.first), std::get<1>(kv.first), std::get<2>(kv.first),
+                     std::get<3>(kv.first), std::get<4>(kv.first), std::get<5>(kv.first), kv.second);
+    return std::fclose(f) == 0 ? QLIN_OK : QLIN_ERR_PARAM;
+}
+
+int qlin_tune_load(const char* path) {
+    if (!path) return QLIN_ERR_PARAM;
+    std::FILE* f = std::fopen(path, "r");
+    if (!f) return QLIN_ERR_PARAM;
+    char line[256];
+    int n = 0, rc = QLIN_OK;
+    std::lock_guard<std::mutex> g(tune_mutex());
+    while (std::fgets(line, sizeof line, f)) {
+        if (line[0] == '#' || line[0] == '\n') continue;
+        int b, K, N, r, path_, swg, v;
+        if (std::sscanf(line, "%d %d %d %d %d %d %d", &b, &K, &N, &r, &path_, &swg, &v) != 7 || (b != 4 && b != 8) ||
+            K <= 0 || N <= 0 || r <= 0 || path_ < 0 || path_ > 2 || (swg != 0 && swg != 1) || v <= 0 ||
+            (path_ < 2 && v != 4 && v != 8 && v != 16)) {
+            rc = QLIN_ERR_PARAM;
+            break;
+        }
+        tune_table()[TuneKey{b, K, N, r, path_, swg}] = v;
+        ++n;
+    }
+    std::fclose(f);
+    return rc ? rc : n;
 }

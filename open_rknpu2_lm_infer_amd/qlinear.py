@@ -160,6 +160,29 @@ class Chain:
             pass
 
 
+def tune(ws: Workspace, w: Weights, rows: int, flags: int = 0, reps: int = 20) -> None:
+    """Time the kernel variants of (w, rows, flags) and record the fastest (qlin_tune)."""
+    check(_lib.load().qlin_tune(ws.handle, w.handle, rows, flags, reps, _stream()), "qlin_tune")
+
+
+def tune_count() -> int:
+    return _lib.load().qlin_tune_count()
+
+
+def tune_clear() -> None:
+    _lib.load().qlin_tune_clear()
+
+
+def tune_save(path: str) -> None:
+    check(_lib.load().qlin_tune_save(path.encode()), "qlin_tune_save")
+
+
+def tune_load(path: str) -> int:
+    n = _lib.load().qlin_tune_load(path.encode())
+    check(min(n, 0), "qlin_tune_load")
+    return n
+
+
 def run(ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor | None = None,
         out_dtype=torch.float16, flags: int = 0, gamma: torch.Tensor | None = None,
         eps: float = 1e-6) -> torch.Tensor:

@@ -10,12 +10,14 @@
 //   npu_backend_test gpu   -- the ported board tests on the GPU
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <functional>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
 
+#include "../../include/qlinear.h"
 #include "../../oracle/qlin_oracle.h"
 #include "../../open_rknpu2_lm_infer_amd/csrc/npu.hpp"
 
@@ -183,6 +185,45 @@ static int gpu_tests() {
                 }
             }
         }
+    }
+    // variant search (the reference's tune_search + tune cache, src/npu.rs:595-615,665-680)
+    {
+        const char* tmp = std::getenv("TMPDIR");
+        const std::string cache = std::string(tmp && *tmp ? tmp : "/tmp") + "/qlin_npu_tune_cache.txt";
+        std::remove(cache.c_str());
+        qlin_tune_clear();
+        npu::ModelOptions topt;
+        topt.chunk = 64;
+        topt.tune_search = true;
+        topt.tune_cache = cache;
+        auto tb = npu::Backend::create(topt, 15);
+        npu::QuantMatrix matrix = padding_matrix(4);
+        std::vector<float> input;
+        for (long i = 0; i < 256 * 256; ++i) input.push_back((float)((i * 17 + i / 256 * 3) % 127) / 63.0f - 1.0f);
+        const std::vector<float> reference = reference_oracle(matrix, input, 256);
+        npu::Linear linear = tb.load(matrix);
+        tb.prepare(1);
+        tb.prepare(64);
+        EXPECT(tb.tune_operations() == 4, "tune operations %zu (plain + SwiGLU at two buckets)", tb.tune_operations());
+        tb.prepare(64);
+        EXPECT(tb.tune_operations() == 4, "a searched bucket was searched again");
+        std::FILE* f = std::fopen(cache.c_str(), "r");
+        EXPECT(f != nullptr, "tune cache not written");
+        if (f) std::fclose(f);
+        for (size_t rows : {1u, 64u}) {
+            std::vector<float> output(rows * 256);
+            linear.run(input.data(), input.size(), output.data(), output.size(), rows);
+            EXPECT(std::memcmp(output.data(), reference.data(), rows * 256 * sizeof(float)) == 0,
+                   "tuned rows %zu: f32 outputs not bit-identical to the oracle", rows);
+        }
+        qlin_tune_clear();
+        npu::ModelOptions lopt;
+        lopt.tune_cache = cache;
+        auto lb = npu::Backend::create(lopt, 15);  // reads the cache
+        EXPECT(qlin_tune_count() >= 2, "tune cache not loaded (%d entries)", qlin_tune_count());
+        EXPECT(lb.tune_operations() == 0, "loading the cache ran a search");
+        qlin_tune_clear();
+        std::remove(cache.c_str());
     }
     return failures;
 }

@@ -347,3 +347,20 @@ def test_graph_replay_matches_eager(ws):
         assert torch.equal(out, eager[0])
     for w, _, _, _ in ws_list:
         w.close()
+
+
+@pytest.mark.parametrize("M", [1, 4, 64])
+def test_lm_head_w8(oracle, M):
+    """W8 output head at the vocabulary width (N = 151,936, K = 2560): one GEMV with 9,496
+    channel groups at decode, the GEMM for a batched scoring pass."""
+    K, N = 2560, 151936
+    codes = synth.codes(N, K, 8, 960).numpy()
+    sc = synth.scales(N, 8, 961).numpy()
+    w = make_weights(8, codes, sc)
+    ws_head = ql.Workspace(64, K, N)
+    A = synth.activations(M, K, seed=962 + M)
+    out = ql.run(ws_head, w, A.to(DEV), out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, False), False, torch.float16)
+    w.close()
+    ws_head.close()
