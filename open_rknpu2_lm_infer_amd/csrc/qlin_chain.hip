@@ -189,22 +189,28 @@ __device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const
     }
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) s_bad[wave] = any_bad;
-    __syncthreads();
-    if (tid == 0) {
-        int b = 0;
-        for (int w = 0; w < kChainWaves; ++w) b |= s_bad[w];
-        if (b && blockIdx.x == 0) atomicOr(p.err, 1u);
-        for (int m = 0; m < M; ++m) {
-            float am = 0.0f;
-            for (int w = 0; w < kChainWaves; ++w) am = fmaxf(am, s_red[w][m]);
-            const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
-            s_rows[m] = s;
-            s_inv[m] = 1.0f / s;
-        }
+    lds_barrier();
+    // per-token scales, computed by every thread from the wave maxima
+    int b = 0;
+#pragma unroll
+    for (int w = 0; w < kChainWaves; ++w) b |= s_bad[w];
+    float inv[MR];
+    bool finite = true;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float am = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kChainWaves; ++w) am = fmaxf(am, s_red[w][m]);
+        const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+        finite &= __builtin_isfinite(s);
+        inv[m] = 1.0f / s;
+        if (tid == 0 && m < M) s_rows[m] = s;
     }
-    __syncthreads();
-    // 4. quantize into LDS (W4: even-k then odd-k bytes per 8-value group)
+    if (tid == 0 && b && blockIdx.x == 0) atomicOr(p.err, 1u);
+    // 4. quantize into LDS (W4: even-k then odd-k bytes per 8-value group); a finite
+    // row (the usual case) takes the short rounding sequence
     const bool rne = (st.flags & kFlagRne) != 0;
+    const bool fast = !b && finite;
     for (int c = tid; c < M * ng; c += kChainThreads) {
         const int m = c / ng, g = c - m * ng;
         float v[8];
@@ -227,10 +233,21 @@ __device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gg[e];
         }
-        const float im = s_inv[m];
-        int q[8];
+        float im = 1.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+        for (int mm = 0; mm < MR; ++mm)
+            if (mm == m) im = inv[mm];
+        int q[8];
+        if (fast && rne) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = quant_finite<true>(v[e], im);
+        } else if (fast) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = quant_finite<false>(v[e], im);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+        }
         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {

@@ -166,6 +166,46 @@ struct XGroup<float> {
     }
 };
 
+// Quantized rows of the fused prologue into LDS for finite rows (quant_finite).
+template <int BITS, bool NORM, bool RNE, int MR, int XR, typename XG>
+__device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float (&gr)[NORM ? XR : 1][8], float nscale,
+                                                const float (&inv)[MR], uint8_t* lds_a, int astride, int nreg, int gpt,
+                                                int ngroups, int tid, int NT) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+        if (i < nreg) {
+            const int m = i / gpt, g = tid + NT * (i - m * gpt);
+            if (g < ngroups) {
+                float v[8];
+                xr[i].get(v);
+                if constexpr (NORM) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                }
+                float im = 1.0f;
+#pragma unroll
+                for (int mm = 0; mm < MR; ++mm)
+                    if (mm == m) im = inv[mm];
+                int q[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) q[e] = quant_finite<RNE>(v[e], im);  // src/npu.rs:1107-1110
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (BITS == 8) {
+                        w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                        w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                    } else {
+                        w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
+                        w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
+                    }
+                }
+                *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
+            }
+        }
+    }
+}
+
 // MODE 0: q/s given.  MODE 1: fused quant of fp16 rows.  MODE 2: fused quant of f32 rows.
 // MR: largest row count of the fused modes (1 or 4).  NORM: RMSNorm before the
 // quantization (fused modes, one row).
@@ -254,15 +294,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                     for (int e = 0; e < 8; ++e) lds_x[8 * g + e] = v[e];
                 }
             }
-            __syncthreads();
+            lds_barrier();
             if (tid < 64) {
                 const float sum = (p.flags & kFlagNormSeq) != 0 ? (tid == 0 ? lds_sumsq_seq(lds_x, p.K) : 0.0f)  // src/ops/norm.rs:38
                                                                 : lds_sumsq_neon16(lds_x, p.K);  // src/model/cpu.rs:14-35
                 if (tid == 0) s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
             }
-            __syncthreads();
+            lds_barrier();
             nscale = s_inv[0];
-            __syncthreads();  // lds_x is overwritten by the quantized row below
+            lds_barrier();  // lds_x is overwritten by the quantized row below
         }
         const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
         if (owner_wave) {
@@ -275,17 +315,27 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                 if (i < nreg) {
                     const int m = i / gpt, g = tid + NT * (i - m * gpt);  // m is uniform
                     if (g < ngroups) {
-                        float v[8];
-                        xr[i].get(v);
+                        float lm;
+                        if constexpr (MODE == 1 && !NORM) {
+                            // fp16 rows: absmax and finiteness from the bit patterns
+                            const uint4 r = xr[i].raw;
+                            const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
+                            bad |= mb > 0x7bffu;
+                            lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                        } else {
+                            float v[8];
+                            xr[i].get(v);
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
-                        if constexpr (NORM) {
+                            for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
+                            if constexpr (NORM) {
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                            }
+                            lm = 0.0f;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
+                            bad |= !__builtin_isfinite(lm);  // the normalized values must stay finite too
                         }
-                        float lm = 0.0f;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
 #pragma unroll
                         for (int mm = 0; mm < MR; ++mm)
                             if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
@@ -301,22 +351,28 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             const bool any_bad = __ballot(bad) != 0;
             if (lane == 0) s_bad[wave] = any_bad;
         }
-        __syncthreads();
-        if (tid == 0) {
-            const int owners = min(WAVES, (ngroups + 63) / 64);
-            int bad_rows = 0;
-            for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
-            if (bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
-            for (int m = 0; m < p.M; ++m) {
-                float am = 0.0f;
-                for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
-                const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
-                s_rows[m] = s;
-                s_inv[m] = 1.0f / s;
-            }
+        lds_barrier();
+        // per-token scales, computed by every thread from the wave maxima
+        const int owners = min(WAVES, (ngroups + 63) / 64);
+        int bad_rows = 0;
+        for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
+        float inv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float am = 0.0f;
+            for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
+            const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+            inv[m] = 1.0f / s;
+            if (tid == 0 && m < p.M) s_rows[m] = s;
         }
-        __syncthreads();
-        if (owner_wave) {
+        if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+        if (owner_wave && !bad_rows) {
+            // finite rows (the usual case): the short rounding sequence
+            if (rne)
+                gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+            else
+                gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+        } else if (owner_wave) {
 #pragma unroll
             for (int i = 0; i < XR; ++i) {
                 if (i < nreg) {
@@ -328,7 +384,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 #pragma unroll
                             for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
                         }
-                        const float im = s_inv[m];
+                        float im = 1.0f;
+#pragma unroll
+                        for (int mm = 0; mm < MR; ++mm)
+                            if (mm == m) im = inv[mm];
                         int q[8];
 #pragma unroll
                         for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
@@ -355,7 +414,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         for (int k = tid * 16; k < p.Kp; k += NT * 16)
             *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 4. stream the weights through the matrix core ---------------------------
     const uint8_t* arow = lds_a + (live ? m_lane : p.M) * astride + (lane >> 4) * (BITS == 4 ? 32 : 16);
@@ -376,7 +435,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     // lane l holds D[4*(l/16) + i][l%16]: only lanes < 16*ceil(ROWS/4) carry real rows
     constexpr int LIVE_LANES = 16 * ((ROWS + 3) / 4);
     constexpr int REGS = ROWS < 4 ? ROWS : 4;
-    __syncthreads();  // the reduction area reuses the activation area
+    lds_barrier();  // the reduction area reuses the activation area
     int* red = reinterpret_cast<int*>(smem);  // [2][WAVES][LIVE_LANES][REGS]
     if (lane < LIVE_LANES) {
 #pragma unroll
@@ -385,7 +444,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             if constexpr (SWIGLU) red[WAVES * LIVE_LANES * REGS + (wave * LIVE_LANES + lane) * REGS + i] = au[i];
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 16 * p.M) {
         const int m = tid >> 4, n = tid & 15;
         const int src = (16 * (m >> 2) + n) * REGS + (m & 3);

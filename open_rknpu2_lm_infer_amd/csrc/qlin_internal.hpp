@@ -113,6 +113,34 @@ __device__ __forceinline__ int quant_one(float x, float inv, bool rne) {
     return (int)r;
 }
 
+// quant_one for a value known finite with |x * inv| < 256, the case of every element
+// of a finite row (|x * inv| <= 127 * (1 + a few ulp)).  Round half away from zero is
+// x + copysign(0.5 - 2^-25, x) truncated by the conversion: equal to Rust's f32::round
+// for every float of magnitude below 256 (checked exhaustively, all 2^31 patterns of
+// that range, against floor(|x| + 0.5) in double precision).  The clamp to +-127 is
+// then a no-op and NaN cannot occur.
+template <bool RNE>
+__device__ __forceinline__ int quant_finite(float x, float inv) {
+    const float v = x * inv;
+    if constexpr (RNE) return (int)__builtin_rintf(v);
+    else return (int)(v + __builtin_copysignf(0.49999997f, v));
+}
+
+// Largest |x| of eight fp16 values (one 16-byte group) as an fp16 bit pattern.
+// Non-negative fp16 values order like their bit patterns, and Inf / NaN (>= 0x7c00)
+// above every finite value, so one unsigned max also flags a non-finite group.
+__device__ __forceinline__ uint32_t absmax_bits_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m = __builtin_bit_cast(u16x2, a & 0x7fff7fffu);
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, b & 0x7fff7fffu));
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, c & 0x7fff7fffu));
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, d & 0x7fff7fffu));
+    return m.x > m.y ? m.x : m.y;
+}
+__device__ __forceinline__ float f32_of_f16_bits(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
 // fp16 store of an f32 result, rounded twice as specified (to f32 by the producing
 // operation, then to fp16 to nearest even).  The empty asm pins x in a VGPR as a
 // rounded f32 value; without it the backend folds the producing multiply into
@@ -128,6 +156,13 @@ __device__ __forceinline__ _Float16 f16_of_f32(float x) {
 // L2 atomics, so completion is all the ordering needed, and the L2 writeback +
 // invalidate of an agent-scope fence is avoided.
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Workgroup barrier that orders LDS accesses only: the caller's LDS operations
+// complete before it, but unlike __syncthreads it does not wait for the caller's
+// outstanding global loads (weight blocks already in flight for later steps).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ void store_coherent(int32_t* p, int32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -13,6 +13,32 @@
 
 namespace qlin {
 
+// Four / eight values -> int8 codes packed little-endian.  `fast` (a finite row, the
+// usual case) takes quant_finite; otherwise quant_one handles Inf / NaN.  The
+// branches are uniform per row.
+__device__ __forceinline__ uint32_t quant4(const float v[4], float inv, bool rne, bool fast) {
+    int q[4];
+    if (fast && rne) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = quant_finite<true>(v[j], inv);
+    } else if (fast) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = quant_finite<false>(v[j], inv);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = quant_one(v[j], inv, rne);  // src/npu.rs:1107-1110
+    }
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w |= (uint32_t)(q[j] & 0xff) << (8 * j);
+    return w;
+}
+__device__ __forceinline__ void quant8(const float v[8], float inv, bool rne, bool fast, uint32_t& w0, uint32_t& w1) {
+    w0 = quant4(v, inv, rne, fast);
+    w1 = quant4(v + 4, inv, rne, fast);
+}
+
+
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(QuantParams p) {
     __shared__ float lds[8];
@@ -25,6 +51,7 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(QuantParams p) 
     const float s = block_row_scale<T, VEC>(x, p.K, p.gamma, gvec, nscale, &bad, lds);
     const float inv = 1.0f / s;
     const bool rne = (p.flags & kFlagRne) != 0;
+    const bool fast = !bad && __builtin_isfinite(s);  // finite row: the short rounding sequence
     const bool qvec = ((reinterpret_cast<uintptr_t>(p.q) & 7) == 0) && (p.ldq % 8 == 0);
     int8_t* qrow = p.q + (int64_t)row * p.ldq;
     for (int k0 = threadIdx.x * 8; k0 < p.ldq; k0 += kRowThreads * 8) {
@@ -35,12 +62,8 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(QuantParams p) 
             load8_gamma(p.gamma, k0, p.K, gvec, g);
             apply_norm8(v, g, nscale);
         }
-        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w0 |= (uint32_t)(quant_one(v[i], inv, rne) & 0xff) << (8 * i);
-            w1 |= (uint32_t)(quant_one(v[4 + i], inv, rne) & 0xff) << (8 * i);
-        }
+        uint32_t w0, w1;
+        quant8(v, inv, rne, fast, w0, w1);
         if (qvec && k0 + 8 <= p.ldq) {
             *reinterpret_cast<uint2*>(qrow + k0) = make_uint2(w0, w1);
         } else {
@@ -142,6 +165,7 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_staged_kernel(QuantPar
     const float s = qscale_from_absmax(m);
     const float inv = 1.0f / s;
     const bool rne = (p.flags & kFlagRne) != 0;
+    const bool fast = !f && __builtin_isfinite(s);  // finite row: the short rounding sequence
     int8_t* qrow = p.q + (int64_t)row * p.ldq;
     // 8 codes per step; the zero tail [K, ldq) too (ldq % 8 == 0 on this path)
     for (int k0 = t * 8; k0 < p.ldq; k0 += kRowThreads * 8) {
@@ -154,11 +178,7 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_staged_kernel(QuantPar
                 load8_gamma(p.gamma, k0, p.K, gvec, g);
                 apply_norm8(v, g, nscale);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                w0 |= (uint32_t)(quant_one(v[i], inv, rne) & 0xff) << (8 * i);
-                w1 |= (uint32_t)(quant_one(v[4 + i], inv, rne) & 0xff) << (8 * i);
-            }
+            quant8(v, inv, rne, fast, w0, w1);
         }
         *reinterpret_cast<uint2*>(qrow + k0) = make_uint2(w0, w1);
     }
@@ -239,6 +259,7 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(QuantParams p, int 
     const float s = qscale_from_absmax(m);
     const float inv = 1.0f / s;
     const bool rne = (p.flags & kFlagRne) != 0;
+    const bool fast = !bad;  // finite row: the short rounding sequence
     int8_t* qrow = p.q + (int64_t)row * p.ldq;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -248,10 +269,10 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(QuantParams p, int 
             uint32_t w[E / 4];
 #pragma unroll
             for (int g = 0; g < E / 4; ++g) {
-                w[g] = 0;
+                float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    w[g] |= (uint32_t)(quant_one(lds_ld(e, 4 * g + j), inv, rne) & 0xff) << (8 * j);
+                for (int j = 0; j < 4; ++j) v[j] = lds_ld(e, 4 * g + j);
+                w[g] = quant4(v, inv, rne, fast);
             }
             if constexpr (E == 8)
                 *reinterpret_cast<uint2*>(qrow + c * E) = make_uint2(w[0], w[1]);
