@@ -493,6 +493,14 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
         if ((waves != 4 && waves != 8 && waves != 16) || (A && !gemv_can_fuse(rows, w->K, waves, gamma != nullptr)))
             waves = gemv_pick_waves(groups, steps);
     }
+    // More items than CUs with the quantization fused: one workgroup per CU (at most
+    // four items each), so each CU quantizes the rows once.
+    const int cus = ws->cu_count;
+    const int grid_env = env_int("QLIN_GEMV_GRID", -1);
+    if (grid_env >= 0)
+        p.grid = grid_env;
+    else if (A && groups > cus)
+        p.grid = std::max(cus, (groups + 3) / 4);
     return launch_gemv(p, w->bits, waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 

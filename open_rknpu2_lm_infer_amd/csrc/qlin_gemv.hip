@@ -48,6 +48,14 @@ struct GemvCfg {
 };
 constexpr int fused_regs(int waves) { return waves >= 16 ? 2 : 8; }
 
+// LDS of gemv_items_kernel: the quantized rows (and the f32 rows of the RMSNorm before
+// them), then the partial-sum area [items][gate, up][WAVES][lanes][regs].
+__host__ __device__ __forceinline__ size_t gemv_red_offset(int M, int Kp, int K, bool fused, bool norm) {
+    size_t a = fused ? (size_t)(M + 1) * (Kp + 16) : 0;
+    if (norm) a = a > (size_t)M * K * sizeof(float) ? a : (size_t)M * K * sizeof(float);
+    return (a + 15) & ~(size_t)15;
+}
+
 template <int BITS>
 __device__ __forceinline__ void a_from_global(v4i a[4], const int8_t* qrow, bool live) {
     const v4i zero = {0, 0, 0, 0};
@@ -109,6 +117,88 @@ __device__ __forceinline__ void compute_batch(v4i& ag, v4i& au, const StepBuf<BA
             }
             mfma_step<BITS>(ag, s.bg[i], a);
             if constexpr (SWIGLU) mfma_step<BITS>(au, s.bu[i], a);
+        }
+    }
+}
+
+// Position in a wave's flat sequence of K steps: item j of the workgroup, step t.
+// The sequence is the workgroup's flat step indices f = j * steps + t that are
+// congruent to the wave index mod WAVES, in increasing order.
+struct GemvPos {
+    int j, t;
+    __device__ __forceinline__ void advance(int waves, int steps) {
+        t += waves;
+        while (t >= steps) {
+            t -= steps;
+            ++j;
+        }
+    }
+};
+
+// Issues the loads of BATCH positions with no branches: positions past the end
+// re-read the last one (an L2 hit), so the compiler can count outstanding loads
+// exactly and never has to wait for more than it consumes.  In the quantized mode
+// the A loads of a position are issued before its weights.
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH>
+__device__ __forceinline__ void load_batch_items(StepBuf<BATCH, FUSED>& s, const GemvParams& p, GemvPos& pos, int& c,
+                                           int total, GemvPos last, const uint8_t* wlane, int64_t up_off,
+                                           const int8_t* qrow, bool live, int steps) {
+    constexpr int KS = BITS == 4 ? 256 : 128;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        const GemvPos q = c < total ? pos : last;
+        const uint8_t* wg = wlane + (int64_t)(16 * ((int)blockIdx.x + q.j * (int)gridDim.x)) * p.wrow +
+                            (int64_t)q.t * 128;
+        if constexpr (!FUSED) a_from_global<BITS>(s.a[i], qrow + q.t * KS, live);
+        s.bg[i][0] = ld16(wg);
+        s.bg[i][1] = ld16(wg + 64);
+        if constexpr (SWIGLU) {
+            s.bu[i][0] = ld16(wg + up_off);
+            s.bu[i][1] = ld16(wg + up_off + 64);
+        }
+        if (c < total) {
+            pos.advance(WAVES, steps);
+            ++c;
+        }
+    }
+}
+
+// Partial sums of the wave's current item to LDS (red[item][gate, up][wave]).
+template <bool SWIGLU, int WAVES, int LIVE, int REGS>
+__device__ __forceinline__ void gemv_flush(int* red, int j, int wave, int lane, v4i& ag, v4i& au) {
+    if (lane < LIVE) {
+#pragma unroll
+        for (int i = 0; i < REGS; ++i) {
+            red[(((j * 2) * WAVES + wave) * LIVE + lane) * REGS + i] = ag[i];
+            if constexpr (SWIGLU) red[(((j * 2 + 1) * WAVES + wave) * LIVE + lane) * REGS + i] = au[i];
+        }
+    }
+    ag = v4i{0, 0, 0, 0};
+    au = v4i{0, 0, 0, 0};
+}
+
+// MFMAs of BATCH positions; cj is the item whose sums ag / au hold.  Moving to a later
+// item flushes them (and zero sums for items this wave has no step of).
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH, int LIVE, int REGS>
+__device__ __forceinline__ void compute_batch_items(v4i& ag, v4i& au, const StepBuf<BATCH, FUSED>& s, const uint8_t* arow,
+                                              GemvPos& pos, int& c, int total, int& cj, int* red, int wave, int lane,
+                                              int steps) {
+    constexpr int KS = BITS == 4 ? 256 : 128;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        if (c < total) {
+            while (cj < pos.j) gemv_flush<SWIGLU, WAVES, LIVE, REGS>(red, cj++, wave, lane, ag, au);
+            v4i a[4];
+            if constexpr (FUSED) {
+                a_from_lds<BITS>(a, arow + pos.t * KS);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = s.a[i][j];
+            }
+            mfma_step<BITS>(ag, s.bg[i], a);
+            if constexpr (SWIGLU) mfma_step<BITS>(au, s.bu[i], a);
+            pos.advance(WAVES, steps);
+            ++c;
         }
     }
 }
@@ -458,11 +548,285 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
 }
 
-size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm) {
-    size_t a = fused ? (size_t)(M + 1) * (Kp + 16) : 0;
-    if (norm) a = std::max(a, (size_t)M * K * sizeof(float));
-    const size_t red = (size_t)2 * waves * 64 * 4 * sizeof(int);
-    return std::max(a, red);
+// Several items per workgroup (fused modes, more items than CUs): the activation
+// prologue as in gemv_kernel, then the flat K-step sequence of the workgroup's items.
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR>
+__global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
+    using T = typename std::conditional<MODE == 2, float, __half>::type;
+    constexpr bool FUSED = MODE != 0;
+    constexpr int NT = 64 * WAVES;
+    constexpr int KS = BITS == 4 ? 256 : 128;
+    constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
+    constexpr int XR = GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_rows[kGemvMaxRows];
+    __shared__ float s_inv[kFusedMaxRows];
+    __shared__ float s_red[WAVES][kFusedMaxRows];
+    __shared__ int s_bad[WAVES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+    const int Nh = p.N >> 1;
+    const int steps = p.Kp / KS;
+    const int groups = (SWIGLU ? Nh : p.Np) >> 4;
+    const int n_items = ((groups - 1 - (int)blockIdx.x) / (int)gridDim.x) + 1;  // items of this workgroup
+    const int flat = n_items * steps;                                             // K steps of the workgroup
+    const int total = wave < flat ? (flat - 1 - wave) / WAVES + 1 : 0;          // of them, this wave's
+    const int m_lane = lane & 15;
+    const bool live = m_lane < p.M;
+    const int m_src = min(m_lane, p.M - 1);
+
+    // ---- 1. activation loads (before any weight load) ---------------------------
+    XGroup<T> xr[FUSED ? XR : 1];
+    float gr[NORM ? XR : 1][8];
+    const int ngroups = p.K >> 3;
+    const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
+    const int nreg = FUSED ? p.M * gpt : 0;   // uniform
+    if constexpr (FUSED) {
+        // Only owned groups are loaded.  These loads may sit in branches because every
+        // weight load below is unconditional: waits for them then count exactly the
+        // weight loads issued after them.
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            if (i < nreg) {
+                const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                if (g < ngroups) xr[i].load(reinterpret_cast<const T*>(p.A) + (int64_t)m * p.lda + 8 * g);
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                const int g = tid + NT * i;
+                if (i < gpt && g < ngroups) {
+                    const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
+                    const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
+                    gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
+                    gr[i][4] = b.x; gr[i][5] = b.y; gr[i][6] = b.z; gr[i][7] = b.w;
+                }
+            }
+        }
+    } else {
+        if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
+    }
+
+    // ---- 2. first weight batch ---------------------------------------------------
+    const uint8_t* wlane = p.W + (int64_t)(lane & 15) * p.wrow + (lane >> 4) * 16;
+    const int64_t up_off = SWIGLU ? (int64_t)Nh * p.wrow : 0;
+    const int8_t* qrow = FUSED ? nullptr : p.q + (int64_t)m_src * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16);
+    StepBuf<BATCH, FUSED> b0, b1;
+    // next position to load, and the last one of the sequence (item 0, step 0 for a
+    // wave without steps, so that its loads below stay in bounds)
+    const int f_last = wave + (total - 1) * WAVES;
+    GemvPos lpos = total > 0 ? GemvPos{wave / steps, wave % steps} : GemvPos{0, 0};
+    const GemvPos last = total > 0 ? GemvPos{f_last / steps, f_last % steps} : GemvPos{0, 0};
+    int lc = 0;
+    // PRE batches in flight during the prologue (two with up to 8 waves, one with 16,
+    // whose 1024 threads already fill the CU's queue); unconditional, so that the waits
+    // for the activation loads above count exactly these loads after them.
+    constexpr int PRE = WAVES <= 8 ? 2 : 1;
+    load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+    if constexpr (PRE == 2) {
+        asm volatile("" ::: "memory");  // keep batch 0's loads ahead of batch 1's
+        load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+    }
+
+    // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
+    // LDS rows 0..M-1 hold the quantized activations; row M is all zeros and feeds
+    // the matrix-core rows M..15.
+    const int astride = p.Kp + 16;
+    uint8_t* lds_a = smem;
+    if constexpr (FUSED) {
+        const bool rne = (p.flags & kFlagRne) != 0;
+        float nscale = 1.0f;
+        if constexpr (NORM) {
+            // the reference summation order needs the whole row in one place
+            float* lds_x = reinterpret_cast<float*>(smem);
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                const int g = tid + NT * i;
+                if (i < gpt && g < ngroups) {
+                    float v[8];
+                    xr[i].get(v);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) lds_x[8 * g + e] = v[e];
+                }
+            }
+            lds_barrier();
+            if (tid < 64) {
+                const float sum = (p.flags & kFlagNormSeq) != 0 ? (tid == 0 ? lds_sumsq_seq(lds_x, p.K) : 0.0f)  // src/ops/norm.rs:38
+                                                                : lds_sumsq_neon16(lds_x, p.K);  // src/model/cpu.rs:14-35
+                if (tid == 0) s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+            }
+            lds_barrier();
+            nscale = s_inv[0];
+            lds_barrier();  // lds_x is overwritten by the quantized row below
+        }
+        const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
+        if (owner_wave) {
+            float mx[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+            int bad = 0;
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                if (i < nreg) {
+                    const int m = i / gpt, g = tid + NT * (i - m * gpt);  // m is uniform
+                    if (g < ngroups) {
+                        float lm;
+                        if constexpr (MODE == 1 && !NORM) {
+                            // fp16 rows: absmax and finiteness from the bit patterns
+                            const uint4 r = xr[i].raw;
+                            const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
+                            bad |= mb > 0x7bffu;
+                            lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                        } else {
+                            float v[8];
+                            xr[i].get(v);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
+                            if constexpr (NORM) {
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                            }
+                            lm = 0.0f;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
+                            bad |= !__builtin_isfinite(lm);  // the normalized values must stay finite too
+                        }
+#pragma unroll
+                        for (int mm = 0; mm < MR; ++mm)
+                            if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < p.M) {
+                    const float w = wave_max_nonneg(mx[m]);
+                    if (lane == 0) s_red[wave][m] = w;
+                }
+            const bool any_bad = __ballot(bad) != 0;
+            if (lane == 0) s_bad[wave] = any_bad;
+        }
+        lds_barrier();
+        // per-token scales, computed by every thread from the wave maxima
+        const int owners = min(WAVES, (ngroups + 63) / 64);
+        int bad_rows = 0;
+        for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
+        float inv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float am = 0.0f;
+            for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
+            const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+            inv[m] = 1.0f / s;
+            if (tid == 0 && m < p.M) s_rows[m] = s;
+        }
+        if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+        if (owner_wave && !bad_rows) {
+            // finite rows (the usual case): the short rounding sequence
+            if (rne)
+                gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+            else
+                gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+        } else if (owner_wave) {
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                if (i < nreg) {
+                    const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                    if (g < ngroups) {
+                        float v[8];
+                        xr[i].get(v);
+                        if constexpr (NORM) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                        }
+                        float im = 1.0f;
+#pragma unroll
+                        for (int mm = 0; mm < MR; ++mm)
+                            if (mm == m) im = inv[mm];
+                        int q[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+                        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if constexpr (BITS == 8) {
+                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                            } else {
+                                w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
+                            }
+                        }
+                        *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
+                    }
+                }
+            }
+        }
+        // zero the K..Kp tail of each row and the whole zero row M
+        for (int m = 0; m < p.M; ++m)
+            for (int k = p.K + tid * 8; k < p.Kp; k += NT * 8)
+                *reinterpret_cast<uint2*>(lds_a + m * astride + k) = make_uint2(0, 0);
+        for (int k = tid * 16; k < p.Kp; k += NT * 16)
+            *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
+    }
+    lds_barrier();
+
+    // ---- 4. stream the weights through the matrix core ---------------------------
+    // lane l holds D[4*(l/16) + i][l%16]: only lanes < 16*ceil(ROWS/4) carry real rows
+    constexpr int LIVE_LANES = 16 * ((ROWS + 3) / 4);
+    constexpr int REGS = ROWS < 4 ? ROWS : 4;
+    int* red = reinterpret_cast<int*>(smem + gemv_red_offset(p.M, p.Kp, p.K, FUSED, NORM));
+    const uint8_t* arow = lds_a + (live ? m_lane : p.M) * astride + (lane >> 4) * (BITS == 4 ? 32 : 16);
+    v4i ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
+    GemvPos cpos{wave / steps, wave % steps};  // next position to multiply
+    int cc = 0, cj = 0;
+    while (cc < total) {
+        if (PRE == 1 && lc < total)
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b0, arow, cpos, cc, total, cj, red,
+                                                                           wave, lane, steps);
+        if (PRE == 2 && lc < total)
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+        if (cc >= total) break;
+        if (PRE == 1 && lc < total)
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b1, arow, cpos, cc, total, cj, red,
+                                                                           wave, lane, steps);
+        if (PRE == 2 && lc < total)
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+    }
+    while (cj < n_items) gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, cj++, wave, lane, ag, au);
+
+    // ---- 5. cross-wave reduction and epilogue ------------------------------------
+    lds_barrier();
+    for (int o = tid; o < n_items * 16 * p.M; o += NT) {
+        const int jj = o / (16 * p.M), rem = o - jj * 16 * p.M;
+        const int m = rem >> 4, n = rem & 15;
+        const int src = (16 * (m >> 2) + n) * REGS + (m & 3);
+        int vg = 0, vu = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            vg += red[((jj * 2) * WAVES + w) * LIVE_LANES * REGS + src];
+            if constexpr (SWIGLU) vu += red[((jj * 2 + 1) * WAVES + w) * LIVE_LANES * REGS + src];
+        }
+        gemv_store<BITS, SWIGLU>(p, m, n, 16 * ((int)blockIdx.x + jj * (int)gridDim.x), vg, vu, s_rows[m]);
+    }
+}
+
+size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm, int items) {
+    if (items <= 1) {
+        // gemv_kernel: the reduction area reuses the activation area
+        size_t a = fused ? (size_t)(M + 1) * (Kp + 16) : 0;
+        if (norm) a = std::max(a, (size_t)M * K * sizeof(float));
+        return std::max(a, (size_t)2 * waves * 64 * 4 * sizeof(int));
+    }
+    const size_t rows = fused ? (M == 1 ? 1 : 4) : kGemvMaxRows;  // rows leaving the matrix core
+    const size_t live = 16 * ((rows + 3) / 4), regs = rows < 4 ? rows : 4;
+    const size_t red = (size_t)items * 2 * waves * live * regs * sizeof(int);
+    return gemv_red_offset(M, Kp, K, fused, norm) + red;
 }
 
 int gemv_pick_waves(int groups, int steps) {
@@ -479,16 +843,35 @@ bool gemv_can_fuse(int M, int K, int waves, bool norm) {
     return true;
 }
 
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR, int WAVES>
+static hipError_t launch_k(const GemvParams& p, dim3 grid, bool items, size_t lds, hipStream_t st) {
+    if (!items) {
+        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>), grid, dim3(64 * WAVES), lds, st, p);
+        return hipGetLastError();
+    }
+    if constexpr (MODE == 0) {
+        return hipErrorInvalidValue;  // several items per workgroup only with fused quantization
+    } else {
+        const void* f = reinterpret_cast<const void*>(&gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>);
+        if (lds > 64 * 1024) {
+            static const hipError_t a = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
+            if (a != hipSuccess) return a;
+        }
+        hipLaunchKernelGGL((gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>), grid, dim3(64 * WAVES), lds, st, p);
+        return hipGetLastError();
+    }
+}
+
 template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR>
 static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
     const int groups = (SWIGLU ? (p.N >> 1) : p.Np) / 16;
-    dim3 grid(groups), block(64 * waves);
+    const bool items = p.grid > 0 && p.grid < groups;
+    const dim3 grid(items ? p.grid : groups);
     switch (waves) {
-        case 4: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 4, MR>), grid, block, lds, st, p); break;
-        case 8: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 8, MR>), grid, block, lds, st, p); break;
-        default: hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, 16, MR>), grid, block, lds, st, p); break;
+        case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4>(p, grid, items, lds, st);
+        case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8>(p, grid, items, lds, st);
+        default: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
     }
-    return hipGetLastError();
 }
 
 template <int BITS, bool SWIGLU, int MODE>
@@ -506,7 +889,10 @@ static hipError_t launch_b(const GemvParams& p, int waves, size_t lds, hipStream
 
 hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream) {
     const bool fused = p.A != nullptr;
-    const size_t lds = gemv_lds_bytes_for(p.M, p.Kp, p.K, waves, fused, fused && p.gamma != nullptr);
+    const int groups = ((p.flags & kFlagSwiglu) ? (p.N >> 1) : p.Np) / 16;
+    const int grid = p.grid > 0 && p.grid < groups ? p.grid : groups;
+    const int items = (groups + grid - 1) / grid;
+    const size_t lds = gemv_lds_bytes_for(p.M, p.Kp, p.K, waves, fused, fused && p.gamma != nullptr, items);
     const bool sw = (p.flags & kFlagSwiglu) != 0;
     if (bits == 4) return sw ? launch_b<4, true>(p, waves, lds, stream) : launch_b<4, false>(p, waves, lds, stream);
     return sw ? launch_b<8, true>(p, waves, lds, stream) : launch_b<8, false>(p, waves, lds, stream);

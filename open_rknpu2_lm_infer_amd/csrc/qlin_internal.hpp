@@ -63,6 +63,7 @@ struct GemvParams {
     int c_kind;         // 0 f32, 1 f16, 2 int32 acc (stage entry point)
     uint32_t flags;
     uint32_t* err;      // bit 0 set on non-finite input (fused quantization)
+    int grid;           // workgroups (each takes items b, b + grid, ...); 0: one per item
 };
 
 struct GemmParams {
@@ -88,7 +89,7 @@ hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream);
 hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream);
 int gemv_pick_waves(int groups, int steps);
 bool gemv_can_fuse(int M, int K, int waves, bool norm);
-size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm);
+size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm, int items);
 hipError_t launch_gemm(const GemmParams& p, int bits, int bn, hipStream_t stream);
 int gemm_tile_n(int bits, int N);          // channels of B per workgroup tile
 int gemm_regs_per_thread(int bn);          // int32 accumulators per thread of one tile
