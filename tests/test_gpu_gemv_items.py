@@ -1,0 +1,73 @@
+"""Decode GEMV with several 16-channel items per workgroup (more items than CUs, fused
+quantization): against the oracle, and bit for bit against the one-item-per-workgroup
+launch of the same shapes (QLIN_GEMV_GRID=0 forces it; the arithmetic is the same)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from open_rknpu2_lm_infer_amd import qlinear as ql
+from open_rknpu2_lm_infer_amd import synth
+from tests.test_gpu_parity import check_outputs, f16_bits, make_weights, oracle_linear
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ws():
+    w = ql.Workspace(8, 4096, 24000)
+    yield w
+    w.close()
+
+
+def run_both(ws, w, A, **kw):
+    """Output of the default launch and of the one-item-per-workgroup launch."""
+    out = ql.run(ws, w, A, **kw)
+    torch.cuda.synchronize()
+    os.environ["QLIN_GEMV_GRID"] = "0"
+    try:
+        ref = ql.run(ws, w, A, **kw)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["QLIN_GEMV_GRID"]
+    return out, ref
+
+
+# item counts: 300 and 1000 plain (2 and 4 per workgroup on 256 CUs), 700 SwiGLU (3 each)
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,swiglu", [(16 * 300, False), (16 * 1000, False), (2 * 16 * 700, True)])
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_items_match_oracle_and_single_item(oracle, ws, bits, N, swiglu, M):
+    K = 1024 if bits == 8 else 2560
+    codes = synth.codes(N, K, bits, 300 + bits).numpy()
+    sc = synth.scales(N, bits, 301 + bits).numpy()
+    w = make_weights(bits, codes, sc)
+    A = synth.activations(M, K, seed=302 + M)
+    flags = ql.QLIN_SWIGLU if swiglu else 0
+    expect = oracle_linear(oracle, A, codes, sc, swiglu)
+    for dt in (torch.float16, torch.float32):
+        out, ref = run_both(ws, w, A.to(DEV).to(dt), out_dtype=torch.float16, flags=flags)
+        assert np.array_equal(f16_bits(out), f16_bits(ref))
+        check_outputs(oracle, out, expect, swiglu, torch.float16)
+    w.close()
+
+
+def test_items_rmsnorm_and_rne(oracle, ws):
+    """RMSNorm prologue and round-half-even with several items per workgroup."""
+    K, N = 2560, 2 * 16 * 600
+    codes = synth.codes(N, K, 4, 310).numpy()
+    sc = synth.scales(N, 4, 311).numpy()
+    w = make_weights(4, codes, sc)
+    A = synth.activations(1, K, seed=312, dist="student_t3")
+    gam = synth.gamma(K, seed=313)
+    out, ref = run_both(ws, w, A.to(DEV), out_dtype=torch.float16, flags=ql.QLIN_SWIGLU, gamma=gam.to(DEV), eps=1e-6)
+    assert np.array_equal(f16_bits(out), f16_bits(ref))
+    check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, True, gamma=gam.numpy()), True, torch.float16)
+    out, ref = run_both(ws, w, A.to(DEV), out_dtype=torch.float16, flags=ql.QLIN_SWIGLU | ql.QLIN_ROUND_HALF_EVEN)
+    assert np.array_equal(f16_bits(out), f16_bits(ref))
+    check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, True, round_mode=oracle.ROUND_EVEN), True,
+                  torch.float16)
+    w.close()
