@@ -563,6 +563,9 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     p.group_m = std::max(1, std::min(p.m_tiles, env_int("QLIN_GEMM_GROUP_M", 4)));
     p.part = ws->gemm_part;
     p.counters = ws->counters;
+    // a grid with at most one workgroup per CU takes the deeper pipeline
+    const int deep_env = env_int("QLIN_GEMM_DEEP", -1);
+    p.deep = deep_env >= 0 ? (deep_env != 0) : (int64_t)tiles * p.splits <= ws->cu_count;
     return launch_gemm(p, w->bits, bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 

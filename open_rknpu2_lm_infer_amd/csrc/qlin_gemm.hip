@@ -229,11 +229,11 @@ __device__ __forceinline__ void interleave() {
 // One k tile: multiply tile t (its first-half A fragments in a0, B in bc); read its
 // second-half A fragments, then, after the barrier, the next tile's first-half A and
 // its B fragments into bn.
-template <int BITS, bool SWIGLU, int BN>
+template <int BITS, bool SWIGLU, int BN, int NSTG>
 __device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], v4i (&a1)[4], const BFrag<BITS, BN>& bc,
                                           BFrag<BITS, BN>& bn, const Copy<BITS, SWIGLU, BN>& cp, uint8_t* smem, int t,
                                           int kt_begin, int last, int abase0, int abase1, int bbase0, int bbase1, int wn) {
-    using G = GemmGeom<BITS, BN>;
+    using G = GemmGeom<BITS, BN, NSTG>;
     constexpr int NMFMA = 4 * G::NI;                          // per half
     constexpr int NREAD_B = BITS == 4 ? G::NI : 2 * G::NI;     // 16-byte B reads per tile
     constexpr int NVALU = BITS == 4 ? 2 : 1;                   // unpack / permute work per MFMA
@@ -253,9 +253,9 @@ __device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], 
     interleave<0, NMFMA, 4 + NREAD_B, G::NL, NVALU>();
 }
 
-template <int BITS, bool SWIGLU, int OUT, int BN>
+template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
-    using G = GemmGeom<BITS, BN>;
+    using G = GemmGeom<BITS, BN, NSTG>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -308,8 +308,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
         read_b<BITS, SWIGLU, BN>(bx, smem + G::A_BYTES, bbase0, bbase1, wn);
 
         for (int t = 0; t < T; t += 2) {
-            gemm_step<BITS, SWIGLU, BN>(acc, a0, a1, bx, by, cp, smem, t, kt_begin, last, abase0, abase1, bbase0, bbase1, wn);
-            gemm_step<BITS, SWIGLU, BN>(acc, a0, a1, by, bx, cp, smem, t + 1, kt_begin, last, abase0, abase1, bbase0, bbase1, wn);
+            gemm_step<BITS, SWIGLU, BN, NSTG>(acc, a0, a1, bx, by, cp, smem, t, kt_begin, last, abase0, abase1, bbase0,
+                                              bbase1, wn);
+            gemm_step<BITS, SWIGLU, BN, NSTG>(acc, a0, a1, by, bx, cp, smem, t + 1, kt_begin, last, abase0, abase1,
+                                              bbase0, bbase1, wn);
         }
         // drain the surplus copies before the LDS is reused or the workgroup ends
         wait_vm<0>();
@@ -436,16 +438,26 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     }
 }
 
-template <int BITS, bool SWIGLU, int OUT, int BN>
-static hipError_t launch_gemm_t(const GemmParams& p, hipStream_t stream) {
-    using G = GemmGeom<BITS, BN>;
+template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG>
+static hipError_t launch_gemm_s(const GemmParams& p, hipStream_t stream) {
+    using G = GemmGeom<BITS, BN, NSTG>;
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_kernel<BITS, SWIGLU, OUT, BN>),
+        reinterpret_cast<const void*>(&gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG>),
         hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (attr != hipSuccess) return attr;
     dim3 grid(p.m_tiles * p.n_tiles * p.splits), block(kGemmThreads);
-    gemm_kernel<BITS, SWIGLU, OUT, BN><<<grid, block, G::LDS, stream>>>(p);
+    gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG><<<grid, block, G::LDS, stream>>>(p);
     return hipGetLastError();
+}
+
+// Stage counts: the default lets two workgroups share a CU (W4); with p.deep (at most
+// one workgroup per CU in the grid) every stage the LDS holds is used, so more k
+// tiles are in flight ahead of the matrix core.
+template <int BITS, bool SWIGLU, int OUT, int BN>
+static hipError_t launch_gemm_t(const GemmParams& p, hipStream_t stream) {
+    constexpr int DEEP = BITS == 4 ? 6 : 4;
+    if (p.deep) return launch_gemm_s<BITS, SWIGLU, OUT, BN, DEEP>(p, stream);
+    return launch_gemm_s<BITS, SWIGLU, OUT, BN, (BITS == 4 ? 3 : 4)>(p, stream);
 }
 
 template <int BITS, int BN>

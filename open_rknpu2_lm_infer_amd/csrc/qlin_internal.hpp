@@ -82,6 +82,7 @@ struct GemmParams {
     int group_m;          // m tiles per group of the tile order
     int32_t* part;        // split-K partials, tile-major
     uint32_t* counters;   // [m_tiles * n_tiles], zero at rest
+    int deep;             // 1: the most LDS stages (grid of at most one workgroup per CU)
 };
 
 // Launchers (return hipError_t of the launch).
