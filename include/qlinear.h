@@ -95,14 +95,15 @@ int qlin_device_query(int32_t device, qlin_device_info* out);
  * reference QuantMatrix layout: int8 [K, N] K-major, codes[k*N + n], values in
  * [-8, 7] for bits = 4 and [-127, 127] for bits = 8; scales f32 [N], positive.
  * Both are host pointers, copied into the current HIP device's HBM as
- * [N, K/2] nibble-packed (low nibble = even k) or [N, K] int8.  Out-of-range
+ * [N, Kp/2] nibble-packed codes (each 32-bit word: byte b holds k = 8w+b low and
+ * 8w+b+4 high, the order the kernels unpack into) or [N, Kp] int8.  Out-of-range
  * codes or non-positive / non-finite scales return QLIN_ERR_PARAM. */
 int qlin_weights_create(const qlin_weight_config* config, const int8_t* codes_kn,
                         const float* scales, qlin_weights** out);
 
-/* Same, from the device layout directly (host pointers): packed is [N, K/2] bytes
- * with the low nibble holding the even k (bits = 4, K even) or [N, K] int8
- * (bits = 8).  Used by the compressed-tensors loader and the benchmark. */
+/* Same, from packed codes (host pointers): packed is [N, K/2] bytes with the low
+ * nibble holding the even k (bits = 4, K even; reordered into the device nibble
+ * order on the device) or [N, K] int8 (bits = 8).  Used by the benchmark. */
 int qlin_weights_create_packed(const qlin_weight_config* config, const void* packed_nk,
                                const float* scales, qlin_weights** out);
 

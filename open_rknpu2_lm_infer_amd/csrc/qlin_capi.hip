@@ -92,6 +92,25 @@ int cu_count(int dev) {
     return n;
 }
 
+// W4 device order.  Each 32-bit word of a row holds the 8 codes of k = 8w .. 8w+7: byte b
+// carries code 8w+b in its low nibble and code 8w+b+4 in its high nibble.  The kernels'
+// unpack ((x << 4) & 0xF0 and x & 0xF0 per byte) then yields the codes in natural k order,
+// so activations are used as they are.  The reference packing (byte j = codes 2j, 2j+1)
+// differs only by a nibble permutation inside each word.
+__host__ __device__ inline uint32_t w4_word_to_device(uint32_t x) {
+    // x: nibble i holds code i (the reference packing of one word)
+    auto spread = [](uint32_t v) {  // nibble i of a 16-bit value -> bits 8i .. 8i+3
+        v = (v | (v << 8)) & 0x00FF00FFu;
+        return (v | (v << 4)) & 0x0F0F0F0Fu;
+    };
+    return spread(x & 0xFFFFu) | (spread(x >> 16) << 4);
+}
+
+__global__ void w4_to_device_kernel(uint32_t* words, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        words[i] = w4_word_to_device(words[i]);
+}
+
 // compressed-tensors rows -> device rows.  W4 pack-quantized: the words' little-endian bytes
 // hold codes 2j (low nibble) and 2j+1 as field = code + 8, whose two's-complement nibble is
 // field ^ 8; W8 pack-quantized: byte ^ 0x80; W8 int-quantized: the byte itself.  Codes at
@@ -103,10 +122,11 @@ __global__ void unpack_compressed_kernel(const uint8_t* src, int64_t src_row, in
         const int64_t r = i / wrow, j = i - r * wrow;
         uint8_t out = 0;
         if (bits == 4) {
-            if (2 * j < K) {
-                const uint8_t b = src[r * src_row + j] ^ 0x88u;
-                out = (uint8_t)((b & 0x0Fu) | (2 * j + 1 < K ? (b & 0xF0u) : 0u));
-            }
+            const int64_t klo = 8 * (j >> 2) + (j & 3), khi = klo + 4;  // device order
+            auto code = [&](int64_t k) -> uint32_t {
+                return k < K ? (((uint32_t)src[r * src_row + (k >> 1)] >> (4 * (k & 1))) & 0xFu) ^ 8u : 0u;
+            };
+            out = (uint8_t)(code(klo) | (code(khi) << 4));
         } else if (j < K) {
             const uint8_t b = src[r * src_row + j];
             out = fmt == 0 ? (uint8_t)(b ^ 0x80u) : b;
@@ -126,9 +146,9 @@ __global__ void pack_kn_kernel(const int8_t* codes, int K, int N, int Kp, int Np
             const int k = j;
             out[i] = (n < N && k < K) ? (uint8_t)codes[(int64_t)k * N + n] : 0;
         } else {
-            const int k = 2 * j;
+            const int k = 8 * (j >> 2) + (j & 3);  // device order: codes k and k + 4
             const int lo = (n < N && k < K) ? codes[(int64_t)k * N + n] : 0;
-            const int hi = (n < N && k + 1 < K) ? codes[(int64_t)(k + 1) * N + n] : 0;
+            const int hi = (n < N && k + 4 < K) ? codes[(int64_t)(k + 4) * N + n] : 0;
             out[i] = (uint8_t)((lo & 0xf) | ((hi & 0xf) << 4));
         }
     }
@@ -271,6 +291,12 @@ static int create_packed(const qlin_weight_config* config, const void* packed, c
     if (hipMemsetAsync(w->W, 0, (size_t)w->Np * w->wrow, st) != hipSuccess ||
         hipMemcpy2DAsync(w->W, (size_t)w->wrow, packed, src_row, src_row, (size_t)config->N, kind, st) != hipSuccess)
         rc = QLIN_ERR_DEVICE;
+    if (!rc && config->bits == 4) {
+        // reference packing -> device order, in place (wrow is a multiple of 4 bytes)
+        hipLaunchKernelGGL(w4_to_device_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<uint32_t*>(w->W),
+                           (int64_t)w->Np * w->wrow / 4);
+        if (hipGetLastError() != hipSuccess) rc = QLIN_ERR_DEVICE;
+    }
     if (!rc) rc = upload_scales(w, scales, kind, st);
     if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = QLIN_ERR_DEVICE;
     if (rc) {

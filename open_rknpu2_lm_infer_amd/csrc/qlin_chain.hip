@@ -207,8 +207,8 @@ __device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const
         if (tid == 0 && m < M) s_rows[m] = s;
     }
     if (tid == 0 && b && blockIdx.x == 0) atomicOr(p.err, 1u);
-    // 4. quantize into LDS (W4: even-k then odd-k bytes per 8-value group); a finite
-    // row (the usual case) takes the short rounding sequence
+    // 4. quantize into LDS (k order for both widths); a finite row (the usual case)
+    // takes the short rounding sequence
     const bool rne = (st.flags & kFlagRne) != 0;
     const bool fast = !b && finite;
     for (int c = tid; c < M * ng; c += kChainThreads) {
@@ -251,13 +251,8 @@ __device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const
         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            if constexpr (BITS == 8) {
-                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-            } else {
-                w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
-                w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
-            }
+            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
         }
         *reinterpret_cast<uint2*>(lds_q + m * astride + 8 * g) = make_uint2(w0, w1);
     }

@@ -15,10 +15,10 @@
 // each 16 bytes unpack in registers into two B operands.  The unpack keeps the
 // nibble in the high half of each byte (w & 0xF0, w << 4 & 0xF0), i.e. 16*code as
 // an exact int8, so the int32 sum is 16x the true one and is shifted back (exact)
-// before dequant.  The two nibble halves come out as even-k / odd-k byte groups,
-// and the activation bytes are put in that same order (in LDS, or by v_perm_b32
-// after a direct load) so the k index of A and B agree lane by lane.  Rows beyond
-// M feed zeros to the matrix core.
+// before dequant.  The device order of W4 codes (byte b of each word holds codes b
+// and b + 4) makes the unpacked bytes come out in natural k order, so activation
+// bytes are used as they are for both widths.  Rows beyond M feed zeros to the
+// matrix core.
 //
 // Ordering.  Memory counters retire in issue order, so every activation load is
 // issued before the first weight load; waiting for the activations then never
@@ -65,8 +65,8 @@ __device__ __forceinline__ void a_from_global(v4i a[4], const int8_t* qrow, bool
     } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            a[2 * j] = perm_evens_odds(live ? ld16(qrow + 128 * j) : zero);           // k 0..15 of the lane's 32
-            a[2 * j + 1] = perm_evens_odds(live ? ld16(qrow + 128 * j + 16) : zero);  // k 16..31
+            a[2 * j] = live ? ld16(qrow + 128 * j) : zero;           // k 0..15 of the lane's 32
+            a[2 * j + 1] = live ? ld16(qrow + 128 * j + 16) : zero;  // k 16..31
         }
     }
 }
@@ -282,13 +282,8 @@ __device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float 
                 uint32_t w0 = 0, w1 = 0;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if constexpr (BITS == 8) {
-                        w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                        w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-                    } else {
-                        w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
-                        w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
-                    }
+                    w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                    w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
                 }
                 *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
             }
@@ -484,13 +479,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            if constexpr (BITS == 8) {
-                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-                            } else {
-                                w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
-                                w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
-                            }
+                            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
                         }
                         *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                     }
@@ -752,13 +742,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            if constexpr (BITS == 8) {
-                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-                            } else {
-                                w0 |= (uint32_t)(q[2 * e] & 0xff) << (8 * e);
-                                w1 |= (uint32_t)(q[2 * e + 1] & 0xff) << (8 * e);
-                            }
+                            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
                         }
                         *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                     }

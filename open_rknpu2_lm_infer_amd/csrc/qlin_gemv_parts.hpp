@@ -11,16 +11,6 @@ __device__ __forceinline__ v4i ld16(const void* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
 
-// even-k then odd-k byte order inside each 8-byte group (matches the W4 unpack)
-__device__ __forceinline__ v4i perm_evens_odds(v4i x) {
-    v4i r;
-    r[0] = (int)__builtin_amdgcn_perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u);  // k0 k2 k4 k6
-    r[1] = (int)__builtin_amdgcn_perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u);  // k1 k3 k5 k7
-    r[2] = (int)__builtin_amdgcn_perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u);
-    r[3] = (int)__builtin_amdgcn_perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u);
-    return r;
-}
-
 template <int BITS>
 __device__ __forceinline__ void mfma_step(v4i& acc, const v4i b[2], const v4i a[4]) {
     if constexpr (BITS == 8) {

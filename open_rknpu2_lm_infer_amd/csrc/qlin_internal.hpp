@@ -1,8 +1,9 @@
 // Internal declarations shared by the HIP translation units of libqlinear.
 //
 // Device layout of the weights (see qlin_capi.hip for the repack):
-//   W4: [Np, Kp/2] bytes, byte j of row n holds k = 2j (low nibble) and 2j+1 (high
-//       nibble) as two's-complement 4-bit codes;
+//   W4: [Np, Kp/2] bytes of two's-complement 4-bit codes; each 32-bit word w of a row
+//       holds k = 8w .. 8w+7, byte b with k = 8w+b in its low nibble and k = 8w+b+4 in
+//       its high nibble (so the kernels' nibble unpack yields k order);
 //   W8: [Np, Kp] int8;
 //   scales: f32 [Np], zero in the padded rows.
 // Kp = roundup(K, 256), Np = roundup(N, 64); pad codes are zero so they add nothing.

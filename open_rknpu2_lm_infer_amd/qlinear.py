@@ -52,7 +52,7 @@ class Weights:
     @classmethod
     def from_packed_device(cls, bits: int, K: int, N: int, packed: torch.Tensor,
                            scales: torch.Tensor) -> "Weights":
-        """Device layout on the GPU: uint8 [N, K/2] (W4) or int8 [N, K] (W8) + f32 [N]."""
+        """Packed codes on the GPU: uint8 [N, K/2] (W4, low nibble = even k) or int8 [N, K] (W8) + f32 [N]."""
         assert packed.is_cuda and scales.is_cuda and packed.is_contiguous() and scales.is_contiguous()
         cfg = _lib.WeightConfig(bits, K, N)
         h = ctypes.c_void_p()
@@ -247,6 +247,7 @@ def run_host_f32(ws: Workspace, w: Weights, A: np.ndarray, swiglu: bool = False)
 
 
 def pack_w4_nk(codes_nk: np.ndarray) -> np.ndarray:
-    """[N, K] codes in [-8, 7] -> [N, K/2] bytes, low nibble = even k (the device layout)."""
+    """[N, K] codes in [-8, 7] -> [N, K/2] bytes, low nibble = even k (the packing the
+    weight-creation entry points take; the library reorders nibbles for its kernels)."""
     c = np.ascontiguousarray(codes_nk, dtype=np.int8).astype(np.uint8) & 0xF
     return (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)

@@ -103,7 +103,7 @@ def stack_scales(N: int, K: int, bits: int, seed: int, device="cpu") -> torch.Te
 
 
 def make_linear(N: int, K: int, bits: int, seed: int, device="cpu", stack: bool = False):
-    """(packed device layout, codes [N,K] int8, scales [N]) for one linear; stack=True
+    """(packed codes (W4: low nibble = even k), codes [N,K] int8, scales [N]) for one linear; stack=True
     draws W8 scales from stack_scales()."""
     c = codes(N, K, bits, seed, device)
     s = stack_scales(N, K, bits, seed + 7, device) if stack else scales(N, bits, seed + 7, device)
