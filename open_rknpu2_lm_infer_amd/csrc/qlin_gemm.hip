@@ -83,7 +83,11 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
+}
 
 // Workgroup barrier without a memory fence: the caller's explicit waits have already
 // completed the LDS reads and copies it orders (a fence would also wait for the copies
@@ -204,20 +208,24 @@ __device__ __forceinline__ void mma_half(v4i (&acc)[4][BN / 32], const v4i (&a)[
     }
 }
 
-// Instruction interleave for the scheduler: MFMA i is followed by one LDS read while
-// any remain (first NDS), one global-to-LDS copy while any remain (first NVM) and
-// VALU instructions.  A wave issues in order and stalls behind an MFMA the matrix
-// core cannot yet take, so reads and copies placed after a run of MFMAs would wait
-// for the whole run; spread out, they issue while the MFMAs execute.
-template <int I, int NMFMA, int NDS, int NVM, int NVALU>
-__device__ __forceinline__ void interleave() {
-    if constexpr (I < NMFMA) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if constexpr (I < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        if constexpr (I < NVM) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-        if constexpr (NVALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
-        interleave<I + 1, NMFMA, NDS, NVM, NVALU>();
+// Instruction order of one half-tile region for the scheduler: the region's global-to-LDS
+// copies and LDS reads first (they only queue work, and what they fetch is used one
+// region later), then per B fragment its unpack VALU work followed by its 4 MFMAs.  A
+// wave issues in order, so reads placed after a run of MFMAs would issue late and the
+// next region would wait for them.
+template <int J, int NJ, int VPJ>
+__device__ __forceinline__ void order_mfma() {
+    if constexpr (J < NJ) {
+        if constexpr (VPJ > 0) __builtin_amdgcn_sched_group_barrier(0x002, VPJ, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        order_mfma<J + 1, NJ, VPJ>();
     }
+}
+template <int NJ, int VPJ, int NDS, int NVM>
+__device__ __forceinline__ void order_region() {
+    if constexpr (NVM > 0) __builtin_amdgcn_sched_group_barrier(0x010, NVM, 0);
+    if constexpr (NDS > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);
+    order_mfma<0, NJ, VPJ>();
 }
 
 // One k tile: multiply tile t (its first-half A fragments in a0, B in bc); read its
@@ -228,14 +236,20 @@ __device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], 
                                           BFrag<BITS, BN>& bn, const Copy<BITS, SWIGLU, BN>& cp, uint8_t* smem, int t,
                                           int kt_begin, int last, int abase0, int abase1, int bbase0, int bbase1, int wn) {
     using G = GemmGeom<BITS, BN, NSTG>;
-    constexpr int NMFMA = 4 * G::NI;                          // per half
     constexpr int NREAD_B = BITS == 4 ? G::NI : 2 * G::NI;     // 16-byte B reads per tile
-    constexpr int NVALU = 1;                                   // unpack work per MFMA
+    constexpr int VPJ = BITS == 4 ? 6 : 0;                     // unpack VALU work per B fragment
     const uint8_t* s0 = smem + (t % G::NST) * G::STAGE;
     read_a(a1, s0, abase1);
     mma_half<BITS, BN>(acc, a0, bc, 0);
-    interleave<0, NMFMA, 4, 0, NVALU>();
-    wait_lgkm0();
+    order_region<G::NI, VPJ, 4, 0>();
+    // Nothing moves across the two fences below: each half's MFMAs then use fragments
+    // read one half (16 MFMAs) earlier instead of waiting on reads just issued.
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage t-1 is refilled below.  This wave read it last in the previous step, and at
+    // least 8 LDS reads were issued after those (LDS reads stay in program order around
+    // the barrier's memory clobbers; their counter retires in order), so waiting until
+    // at most the 4 reads of a1 are outstanding completes them without waiting for a1.
+    wait_lgkm<4>();
     wait_vm<(G::NST - 3) * G::NL>();  // own copies of tile t+1 have landed
     barrier_no_fence();               // everyone's have, and stage t-1 is free
     const int fill = t + G::NST - 1;
@@ -244,7 +258,8 @@ __device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], 
     read_a(a0, s1, abase0);
     read_b<BITS, SWIGLU, BN>(bn, s1 + G::A_BYTES, bbase0, bbase1, wn);
     mma_half<BITS, BN>(acc, a1, bc, 1);
-    interleave<0, NMFMA, 4 + NREAD_B, G::NL, NVALU>();
+    order_region<G::NI, VPJ, 4 + NREAD_B, G::NL>();
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG>

@@ -204,7 +204,8 @@ __device__ __forceinline__ void compute_batch_items(v4i& ag, v4i& au, const Step
 }
 
 template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, int r0, int vg, int vu, float sm) {
+__device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, int r0, int vg, int vu, float sm,
+                                           float wsg, float wsu) {
     const int Nh = p.N >> 1;
     const int ag = BITS == 4 ? (vg >> 4) : vg;  // exact: W4 sums carry a factor 16
     const int cg = r0 + n;
@@ -212,10 +213,10 @@ __device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, in
         if (cg < p.N) reinterpret_cast<int32_t*>(p.C)[(int64_t)m * p.ldc + cg] = ag;
         return;
     }
-    float out = ((float)ag * sm) * p.wscale[cg];  // src/npu.rs:1117
+    float out = ((float)ag * sm) * wsg;  // src/npu.rs:1117 (wsg = wscale[cg])
     if constexpr (SWIGLU) {
         const int au = BITS == 4 ? (vu >> 4) : vu;
-        const float up = ((float)au * sm) * p.wscale[Nh + cg];
+        const float up = ((float)au * sm) * wsu;  // wsu = wscale[N/2 + cg]
         out = (out / (1.0f + expf(-out))) * up;  // src/npu.rs:1202-1208
     }
     if (cg < (SWIGLU ? Nh : p.N)) {
@@ -317,7 +318,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const bool live = m_lane < p.M;
     const int m_src = min(m_lane, p.M - 1);
 
-    // ---- 1. activation loads (before any weight load) ---------------------------
+    // ---- 1. channel scales and activation loads (before any weight load) ---------
+    // the scales of this thread's epilogue outputs, so the epilogue needs no memory trip
+    float wsg = 0.0f, wsu = 0.0f;
+    if (tid < 16 * p.M) {
+        wsg = p.wscale[r0 + (tid & 15)];
+        if constexpr (SWIGLU) wsu = p.wscale[(p.N >> 1) + r0 + (tid & 15)];
+    }
     XGroup<T> xr[FUSED ? XR : 1];
     float gr[NORM ? XR : 1][8];
     const int ngroups = p.K >> 3;
@@ -534,7 +541,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             vg += red[w * LIVE_LANES * REGS + src];
             if constexpr (SWIGLU) vu += red[WAVES * LIVE_LANES * REGS + w * LIVE_LANES * REGS + src];
         }
-        gemv_store<BITS, SWIGLU>(p, m, n, r0, vg, vu, s_rows[m]);
+        gemv_store<BITS, SWIGLU>(p, m, n, r0, vg, vu, s_rows[m], wsg, wsu);
     }
 }
 
@@ -567,7 +574,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     const bool live = m_lane < p.M;
     const int m_src = min(m_lane, p.M - 1);
 
-    // ---- 1. activation loads (before any weight load) ---------------------------
+    // ---- 1. channel scales and activation loads (before any weight load) ---------
+    // the scales of this thread's first epilogue output (the only one unless the
+    // outputs outnumber the threads)
+    float wsg = 0.0f, wsu = 0.0f;
+    if (tid < n_items * 16 * p.M) {
+        const int cg = 16 * ((int)blockIdx.x + (tid / (16 * p.M)) * (int)gridDim.x) + (tid & 15);
+        wsg = p.wscale[cg];
+        if constexpr (SWIGLU) wsu = p.wscale[Nh + cg];
+    }
     XGroup<T> xr[FUSED ? XR : 1];
     float gr[NORM ? XR : 1][8];
     const int ngroups = p.K >> 3;
@@ -797,7 +812,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             vg += red[((jj * 2) * WAVES + w) * LIVE_LANES * REGS + src];
             if constexpr (SWIGLU) vu += red[((jj * 2 + 1) * WAVES + w) * LIVE_LANES * REGS + src];
         }
-        gemv_store<BITS, SWIGLU>(p, m, n, 16 * ((int)blockIdx.x + jj * (int)gridDim.x), vg, vu, s_rows[m]);
+        const int r0 = 16 * ((int)blockIdx.x + jj * (int)gridDim.x);
+        if (o != tid) {
+            wsg = p.wscale[r0 + n];
+            if constexpr (SWIGLU) wsu = p.wscale[Nh + r0 + n];
+        }
+        gemv_store<BITS, SWIGLU>(p, m, n, r0, vg, vu, s_rows[m], wsg, wsu);
     }
 }
 
