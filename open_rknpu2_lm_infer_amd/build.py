@@ -1,5 +1,6 @@
 """Builds libqlinear.so (the HIP kernels, the C ABI and the C++ npu mirror) in-tree
-for gfx950, and the native test binary tests/cpp/_build/npu_backend_test.
+for gfx950, the native test binary tests/cpp/_build/npu_backend_test and the hardware
+calibration probes probes/_build/hw_probes.
 
     python -m open_rknpu2_lm_infer_amd.build
 
@@ -45,6 +46,8 @@ ROOT = os.path.dirname(HERE)
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "npu_backend_test.cpp")
 TEST_BUILD = os.path.join(ROOT, "tests", "cpp", "_build")
 TEST_BIN = os.path.join(TEST_BUILD, "npu_backend_test")
+PROBE_SRC = os.path.join(HERE, "probes", "hw_probes.hip")
+PROBE_BIN = os.path.join(HERE, "probes", "_build", "hw_probes")
 
 
 def sources():
@@ -78,6 +81,7 @@ def build(verbose: bool = False) -> str:
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     build_tests()
+    build_probes()
     return LIB
 
 
@@ -90,6 +94,15 @@ def build_tests() -> str:
     subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", TEST_SRC, oracle_obj, "-o", TEST_BIN,
                     f"-L{HERE}", "-lqlinear", "-Wl,-rpath,$ORIGIN/../../../open_rknpu2_lm_infer_amd", "-lm"], check=True)
     return TEST_BIN
+
+
+def build_probes() -> str:
+    """Calibration probes (MFMA rate, LDS copy rate, LDS read patterns, launch floors);
+    the MFMA chains stay in VGPRs as in the GEMM."""
+    os.makedirs(os.path.dirname(PROBE_BIN), exist_ok=True)
+    subprocess.run([HIPCC, *[f for f in COMMON if f not in ("-fPIC",)], "-mllvm", "-amdgpu-mfma-vgpr-form",
+                    PROBE_SRC, "-o", PROBE_BIN], check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    return PROBE_BIN
 
 
 if __name__ == "__main__":
