@@ -626,10 +626,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     GemvPos lpos = total > 0 ? GemvPos{wave / steps, wave % steps} : GemvPos{0, 0};
     const GemvPos last = total > 0 ? GemvPos{f_last / steps, f_last % steps} : GemvPos{0, 0};
     int lc = 0;
-    // PRE batches in flight during the prologue (two with up to 8 waves, one with 16,
-    // whose 1024 threads already fill the CU's queue); unconditional, so that the waits
-    // for the activation loads above count exactly these loads after them.
-    constexpr int PRE = WAVES <= 8 ? 2 : 1;
+    // PRE batches in flight during the prologue: two with up to 8 waves; one with 16,
+    // whose 1024 threads already fill the CU's queue, and one with SwiGLU, whose steps
+    // load twice the bytes (two batches there delayed the prologue: gate_up 2560x19456
+    // 9.55 -> 8.89 us with one).  Unconditional, so that the waits for the activation
+    // loads above count exactly these loads after them.
+    constexpr int PRE = WAVES <= 8 && !SWIGLU ? 2 : 1;
     load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
     if constexpr (PRE == 2) {
         asm volatile("" ::: "memory");  // keep batch 0's loads ahead of batch 1's
