@@ -3,6 +3,8 @@
 // synchronous rk_npu_w4a8_run_f32 / rk_npu_f32i8f32_run_dynamic.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -87,8 +89,11 @@ int tuned_variant(int bits, int K, int N, int rows, int path, bool sw) {
 
 
 int cu_count(int dev) {
+    static std::atomic<int> cached[64] = {};  // per device, 0 = not read yet
+    if (dev >= 0 && dev < 64 && cached[dev].load(std::memory_order_relaxed) > 0) return cached[dev].load(std::memory_order_relaxed);
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (dev >= 0 && dev < 64) cached[dev].store(n, std::memory_order_relaxed);
     return n;
 }
 
@@ -484,6 +489,14 @@ int qlin_quantize(int32_t rows, int32_t K, const void* A, int32_t a_dtype, int64
 
 namespace {
 
+// Output channels per GEMV item: QLIN_GEMV_ITEM_WIDTH (1..16) if set, else the width in
+// 8..16 that spreads the items most evenly over the CUs.
+int gemv_width(const qlin_weights* w, bool sw, int cus) {
+    const int forced = env_int("QLIN_GEMV_ITEM_WIDTH", 0);
+    if (forced >= 1 && forced <= 16) return forced;
+    return gemv_item_width(sw ? w->N / 2 : w->N, cus);
+}
+
 int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
              const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
              int64_t ldc, uint32_t flags, hipStream_t st) {
@@ -511,7 +524,8 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     p.flags = flags;
     p.err = ws->err;
     const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
-    const int groups = (sw ? w->N / 2 : w->Np) / 16;
+    p.iw = gemv_width(w, sw, ws->cu_count);
+    const int groups = gemv_items(p);
     int waves = env_int("QLIN_GEMV_WAVES", 0);
     if (waves != 4 && waves != 8 && waves != 16) {
         waves = tuned_variant(w->bits, w->K, w->N, rows, A ? 0 : 1, sw);
@@ -538,7 +552,9 @@ bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, c
         return false;
     const bool sw = (flags & kFlagSwiglu) != 0;
     const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
-    const int waves = gemv_pick_waves((sw ? w->N / 2 : w->Np) / 16, steps);
+    const int cols = sw ? w->N / 2 : w->N;
+    const int iw = gemv_width(w, sw, cu_count(w->device));
+    const int waves = gemv_pick_waves((cols + iw - 1) / iw, steps);
     return gemv_can_fuse(rows, w->K, waves, gamma != nullptr) &&
            (env_int("QLIN_GEMV_WAVES", 0) == 0 || gemv_can_fuse(rows, w->K, env_int("QLIN_GEMV_WAVES", 0), gamma != nullptr));
 }

@@ -142,13 +142,14 @@ struct GemvPos {
 template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH>
 __device__ __forceinline__ void load_batch_items(StepBuf<BATCH, FUSED>& s, const GemvParams& p, GemvPos& pos, int& c,
                                            int total, GemvPos last, const uint8_t* wlane, int64_t up_off,
-                                           const int8_t* qrow, bool live, int steps) {
+                                           const int8_t* qrow, bool live, int steps, int lrow, int ncols) {
     constexpr int KS = BITS == 4 ? 256 : 128;
 #pragma unroll
     for (int i = 0; i < BATCH; ++i) {
         const GemvPos q = c < total ? pos : last;
-        const uint8_t* wg = wlane + (int64_t)(16 * ((int)blockIdx.x + q.j * (int)gridDim.x)) * p.wrow +
-                            (int64_t)q.t * 128;
+        // weight row of this lane: row lrow of the item, the last real row past the end
+        const int row = min(p.iw * ((int)blockIdx.x + q.j * (int)gridDim.x) + lrow, ncols - 1);
+        const uint8_t* wg = wlane + (int64_t)row * p.wrow + (int64_t)q.t * 128;
         if constexpr (!FUSED) a_from_global<BITS>(s.a[i], qrow + q.t * KS, live);
         s.bg[i][0] = ld16(wg);
         s.bg[i][1] = ld16(wg + 64);
@@ -311,7 +312,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     __shared__ int s_bad[WAVES];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = blockIdx.x * 16;
+    const int r0 = blockIdx.x * p.iw;  // first output channel of the item
+    const int ncols = gemv_out_cols(p);
     const int Nh = p.N >> 1;
     const int steps = p.Kp / KS;
     const int m_lane = lane & 15;
@@ -322,8 +324,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     // the scales of this thread's epilogue outputs, so the epilogue needs no memory trip
     float wsg = 0.0f, wsu = 0.0f;
     if (tid < 16 * p.M) {
-        wsg = p.wscale[r0 + (tid & 15)];
-        if constexpr (SWIGLU) wsu = p.wscale[(p.N >> 1) + r0 + (tid & 15)];
+        const int cg = min(r0 + (tid & 15), ncols - 1);
+        wsg = p.wscale[cg];
+        if constexpr (SWIGLU) wsu = p.wscale[(p.N >> 1) + cg];
     }
     XGroup<T> xr[FUSED ? XR : 1];
     float gr[NORM ? XR : 1][8];
@@ -358,8 +361,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
 
     // ---- 2. first weight batch ---------------------------------------------------
-    const uint8_t* wg = p.W + (int64_t)(r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16;
-    const uint8_t* wu = SWIGLU ? p.W + (int64_t)(Nh + r0 + (lane & 15)) * p.wrow + (lane >> 4) * 16 : nullptr;
+    // lane rows past the item's width (or past the last channel) re-read its last row
+    const int wrow_l = min(r0 + min(lane & 15, p.iw - 1), ncols - 1);
+    const uint8_t* wg = p.W + (int64_t)wrow_l * p.wrow + (lane >> 4) * 16;
+    const uint8_t* wu = SWIGLU ? p.W + (int64_t)(Nh + wrow_l) * p.wrow + (lane >> 4) * 16 : nullptr;
     const int8_t* qrow = FUSED ? nullptr : p.q + (int64_t)m_src * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16);
     StepBuf<BATCH, FUSED> b0, b1;
     int base = wave;
@@ -532,7 +537,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         }
     }
     lds_barrier();
-    if (tid < 16 * p.M) {
+    if (tid < 16 * p.M && (tid & 15) < p.iw) {
         const int m = tid >> 4, n = tid & 15;
         const int src = (16 * (m >> 2) + n) * REGS + (m & 3);
         int vg = 0, vu = 0;
@@ -566,7 +571,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
     const int Nh = p.N >> 1;
     const int steps = p.Kp / KS;
-    const int groups = (SWIGLU ? Nh : p.Np) >> 4;
+    const int groups = gemv_items(p);
+    const int ncols = gemv_out_cols(p);
     const int n_items = ((groups - 1 - (int)blockIdx.x) / (int)gridDim.x) + 1;  // items of this workgroup
     const int flat = n_items * steps;                                             // K steps of the workgroup
     const int total = wave < flat ? (flat - 1 - wave) / WAVES + 1 : 0;          // of them, this wave's
@@ -579,7 +585,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     // outputs outnumber the threads)
     float wsg = 0.0f, wsu = 0.0f;
     if (tid < n_items * 16 * p.M) {
-        const int cg = 16 * ((int)blockIdx.x + (tid / (16 * p.M)) * (int)gridDim.x) + (tid & 15);
+        const int cg = min(p.iw * ((int)blockIdx.x + (tid / (16 * p.M)) * (int)gridDim.x) + (tid & 15), ncols - 1);
         wsg = p.wscale[cg];
         if constexpr (SWIGLU) wsu = p.wscale[Nh + cg];
     }
@@ -616,7 +622,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     }
 
     // ---- 2. first weight batch ---------------------------------------------------
-    const uint8_t* wlane = p.W + (int64_t)(lane & 15) * p.wrow + (lane >> 4) * 16;
+    const int lrow = min(lane & 15, p.iw - 1);  // row of the item this lane loads
+    const uint8_t* wlane = p.W + (lane >> 4) * 16;
     const int64_t up_off = SWIGLU ? (int64_t)Nh * p.wrow : 0;
     const int8_t* qrow = FUSED ? nullptr : p.q + (int64_t)m_src * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16);
     StepBuf<BATCH, FUSED> b0, b1;
@@ -632,10 +639,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     // 9.55 -> 8.89 us with one).  Unconditional, so that the waits for the activation
     // loads above count exactly these loads after them.
     constexpr int PRE = WAVES <= 8 && !SWIGLU ? 2 : 1;
-    load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+    load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
     if constexpr (PRE == 2) {
         asm volatile("" ::: "memory");  // keep batch 0's loads ahead of batch 1's
-        load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+        load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
     }
 
     // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
@@ -787,18 +794,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     int cc = 0, cj = 0;
     while (cc < total) {
         if (PRE == 1 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
         compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b0, arow, cpos, cc, total, cj, red,
                                                                            wave, lane, steps);
         if (PRE == 2 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
         if (cc >= total) break;
         if (PRE == 1 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
         compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b1, arow, cpos, cc, total, cj, red,
                                                                            wave, lane, steps);
         if (PRE == 2 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
     }
     while (cj < n_items) gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, cj++, wave, lane, ag, au);
 
@@ -814,10 +821,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             vg += red[((jj * 2) * WAVES + w) * LIVE_LANES * REGS + src];
             if constexpr (SWIGLU) vu += red[((jj * 2 + 1) * WAVES + w) * LIVE_LANES * REGS + src];
         }
-        const int r0 = 16 * ((int)blockIdx.x + jj * (int)gridDim.x);
+        const int r0 = p.iw * ((int)blockIdx.x + jj * (int)gridDim.x);
+        if (n >= p.iw) continue;  // a re-read row, not an output
         if (o != tid) {
-            wsg = p.wscale[r0 + n];
-            if constexpr (SWIGLU) wsu = p.wscale[Nh + r0 + n];
+            wsg = p.wscale[min(r0 + n, ncols - 1)];
+            if constexpr (SWIGLU) wsu = p.wscale[Nh + min(r0 + n, ncols - 1)];
         }
         gemv_store<BITS, SWIGLU>(p, m, n, r0, vg, vu, s_rows[m], wsg, wsu);
     }
@@ -834,6 +842,17 @@ size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm
     const size_t live = 16 * ((rows + 3) / 4), regs = rows < 4 ? rows : 4;
     const size_t red = (size_t)items * 2 * waves * live * regs * sizeof(int);
     return gemv_red_offset(M, Kp, K, fused, norm) + red;
+}
+
+int gemv_item_width(int cols, int cus) {
+    // The busiest CU streams (items per CU) x iw weight rows; take the widest iw within 3%
+    // of the fewest such rows (narrower items re-read rows, L2 hits, and add positions).
+    auto rows_on_busiest = [&](int iw) { return ((cols + iw - 1) / iw + cus - 1) / cus * iw; };
+    int least = rows_on_busiest(16);
+    for (int iw = 15; iw >= 8; --iw) least = std::min(least, rows_on_busiest(iw));
+    for (int iw = 16; iw > 8; --iw)
+        if (rows_on_busiest(iw) * 100 <= least * 103) return iw;
+    return 8;
 }
 
 int gemv_pick_waves(int groups, int steps) {
@@ -871,7 +890,7 @@ static hipError_t launch_k(const GemvParams& p, dim3 grid, bool items, size_t ld
 
 template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR>
 static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
-    const int groups = (SWIGLU ? (p.N >> 1) : p.Np) / 16;
+    const int groups = gemv_items(p);
     const bool items = p.grid > 0 && p.grid < groups;
     const dim3 grid(items ? p.grid : groups);
     switch (waves) {
@@ -896,7 +915,8 @@ static hipError_t launch_b(const GemvParams& p, int waves, size_t lds, hipStream
 
 hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream) {
     const bool fused = p.A != nullptr;
-    const int groups = ((p.flags & kFlagSwiglu) ? (p.N >> 1) : p.Np) / 16;
+    if (p.iw < 1 || p.iw > 16) return hipErrorInvalidValue;
+    const int groups = gemv_items(p);
     const int grid = p.grid > 0 && p.grid < groups ? p.grid : groups;
     const int items = (groups + grid - 1) / grid;
     const size_t lds = gemv_lds_bytes_for(p.M, p.Kp, p.K, waves, fused, fused && p.gamma != nullptr, items);

@@ -65,7 +65,17 @@ struct GemvParams {
     uint32_t flags;
     uint32_t* err;      // bit 0 set on non-finite input (fused quantization)
     int grid;           // workgroups (each takes items b, b + grid, ...); 0: one per item
+    int iw;             // output channels per item, 1..16 (the MFMA tile's 16 rows; rows past
+                        // iw re-read the item's last row and are not stored)
 };
+
+// Items of a GEMV launch: output channels (N, or N/2 with SwiGLU) in groups of iw.
+__host__ __device__ __forceinline__ int gemv_out_cols(const GemvParams& p) {
+    return (p.flags & kFlagSwiglu) ? (p.N >> 1) : p.N;
+}
+__host__ __device__ __forceinline__ int gemv_items(const GemvParams& p) {
+    return (gemv_out_cols(p) + p.iw - 1) / p.iw;
+}
 
 struct GemmParams {
     const uint8_t* W;
@@ -90,6 +100,7 @@ struct GemmParams {
 hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream);
 hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream);
 int gemv_pick_waves(int groups, int steps);
+int gemv_item_width(int cols, int cus);  // iw in 8..16 spreading cols / iw items best over the CUs
 bool gemv_can_fuse(int M, int K, int waves, bool norm);
 size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm, int items);
 hipError_t launch_gemm(const GemmParams& p, int bits, int bn, hipStream_t stream);

@@ -71,3 +71,29 @@ def test_items_rmsnorm_and_rne(oracle, ws):
     check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, True, round_mode=oracle.ROUND_EVEN), True,
                   torch.float16)
     w.close()
+
+
+@pytest.mark.parametrize("iw", [1, 5, 10, 13, 16])
+@pytest.mark.parametrize("bits,N,swiglu", [(4, 2560, False), (8, 2 * 1312, True), (4, 6144, False)])
+def test_item_width_matches_oracle(oracle, ws, iw, bits, N, swiglu):
+    """Items narrower than the 16-row MFMA tile (QLIN_GEMV_ITEM_WIDTH): rows past the width
+    re-read the item's last row and are not stored; every output channel once, bit for bit
+    equal to the default width and within the bar of the oracle, fused and unfused."""
+    K = 2560
+    codes = synth.codes(N, K, bits, 320 + iw).numpy()
+    sc = synth.scales(N, bits, 321 + iw).numpy()
+    w = make_weights(bits, codes, sc)
+    flags = ql.QLIN_SWIGLU if swiglu else 0
+    for M, extra in ((1, 0), (3, 0), (1, ql.QLIN_NO_FUSED_QUANT)):
+        A = synth.activations(M, K, seed=322 + M)
+        ref = ql.run(ws, w, A.to(DEV), out_dtype=torch.float16, flags=flags | extra)
+        torch.cuda.synchronize()
+        os.environ["QLIN_GEMV_ITEM_WIDTH"] = str(iw)
+        try:
+            out = ql.run(ws, w, A.to(DEV), out_dtype=torch.float16, flags=flags | extra)
+            torch.cuda.synchronize()
+        finally:
+            del os.environ["QLIN_GEMV_ITEM_WIDTH"]
+        assert np.array_equal(f16_bits(out), f16_bits(ref))
+        check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, swiglu), swiglu, torch.float16)
+    w.close()
