@@ -32,7 +32,6 @@ struct qlin_workspace {
     int max_rows, max_k, max_n, max_kp, max_np, device, cu_count;
     int8_t* q;           // [max_rows, max_kp]
     float* s;            // [max_rows]
-    int32_t* gemv_part;  // [kGemvMaxRows, max_np], zero at rest
     uint32_t* counters;  // [n_counters], zero at rest
     int n_counters;
     int32_t* gemm_part;  // [kGemmPartInts]
@@ -407,20 +406,19 @@ int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_w
     ws->cu_count = cu_count(dev);
     ws->n_counters = std::max(ws->max_np / 16, 8192);
     const size_t bq = (size_t)max_rows * ws->max_kp, bs = (size_t)max_rows * sizeof(float);
-    const size_t bgp = (size_t)kGemvMaxRows * ws->max_np * sizeof(int32_t);
     const size_t bc = (size_t)ws->n_counters * sizeof(uint32_t);
     const size_t bgm = (size_t)kGemmPartInts * sizeof(int32_t);
     const size_t bA = (size_t)max_rows * max_k * sizeof(float), bC = (size_t)max_rows * max_n * sizeof(float);
     bool ok = hipMalloc(&ws->q, bq) == hipSuccess && hipMalloc(&ws->s, bs) == hipSuccess &&
-              hipMalloc(&ws->gemv_part, bgp) == hipSuccess && hipMalloc(&ws->counters, bc) == hipSuccess &&
+              hipMalloc(&ws->counters, bc) == hipSuccess &&
               hipMalloc(&ws->gemm_part, bgm) == hipSuccess && hipMalloc(&ws->err, 256) == hipSuccess &&
               hipMalloc(&ws->dA, bA) == hipSuccess && hipMalloc(&ws->dC, bC) == hipSuccess &&
               hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess;
     if (ok)
-        ok = hipMemset(ws->gemv_part, 0, bgp) == hipSuccess && hipMemset(ws->counters, 0, bc) == hipSuccess &&
+        ok = hipMemset(ws->counters, 0, bc) == hipSuccess &&
              hipMemset(ws->err, 0, 256) == hipSuccess && hipMemset(ws->q, 0, bq) == hipSuccess &&
              hipDeviceSynchronize() == hipSuccess;
-    ws->device_bytes = bq + bs + bgp + bc + bgm + 256 + bA + bC;
+    ws->device_bytes = bq + bs + bc + bgm + 256 + bA + bC;
     ws->last = ws->stream;
     if (!ok) {
         qlin_workspace_free(ws);
@@ -438,7 +436,6 @@ void qlin_workspace_free(qlin_workspace* ws) {
     }
     (void)hipFree(ws->q);
     (void)hipFree(ws->s);
-    (void)hipFree(ws->gemv_part);
     (void)hipFree(ws->counters);
     (void)hipFree(ws->gemm_part);
     (void)hipFree(ws->err);

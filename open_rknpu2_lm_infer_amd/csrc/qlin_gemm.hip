@@ -307,6 +307,28 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < G::NI; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
+    // Epilogue scales, loaded before the first copy so their round trip overlaps the k
+    // loop.  Lane (fr, fc) holds, for A fragment i and B fragment j, row m0 + 64 wm + 16 i
+    // + fr at the 4 consecutive channels cbase + 16 j + r.  (Older than every copy, they
+    // retire before the first copy wait, which counts only copies issued after them.)
+    constexpr int NJ = SWIGLU ? G::NI / 2 : G::NI;
+    const int mrow = m0 + wm * 64 + fr;
+    const int cbase = n0 + wn * (SWIGLU ? BN / 4 : BN / 2) + 4 * fc;
+    const int ncols = SWIGLU ? (p.N >> 1) : p.N;
+    float sm[4];
+    float4 sg[NJ], su[SWIGLU ? NJ : 1];
+    if constexpr (OUT != 2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm[i] = p.s[min(mrow + 16 * i, p.M - 1)];
+        const int cmax = (SWIGLU ? ncols : p.Np) - 4;  // scales hold Np entries
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int c = min(cbase + 16 * j, cmax);
+            sg[j] = *reinterpret_cast<const float4*>(p.wscale + c);
+            if constexpr (SWIGLU) su[j] = *reinterpret_cast<const float4*>(p.wscale + (p.N >> 1) + c);
+        }
+    }
+
     {
         const Copy<BITS, SWIGLU, BN> cp(p, m0, n0, wave, lane);
 #pragma unroll
@@ -360,31 +382,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
         if (tid == 0) atomicExch(&p.counters[tile], 0u);
     }
 
-    // Epilogue.  Lane (fr, fc) holds, for A fragment i and B fragment j, row
-    // m0 + 64 wm + 16 i + fr at the 4 consecutive channels cbase + 16 j + r.  All scales
-    // are loaded first (one memory round trip), then each 4-channel group is written
-    // with one vector store when the row stride and base allow it.
-    constexpr int NJ = SWIGLU ? G::NI / 2 : G::NI;
-    const int mrow = m0 + wm * 64 + fr;
-    const int cbase = n0 + wn * (SWIGLU ? BN / 4 : BN / 2) + 4 * fc;
-    const int ncols = SWIGLU ? (p.N >> 1) : p.N;
+    // Epilogue: each 4-channel group is written with one vector store when the row
+    // stride and base allow it (the scales were loaded before the k loop).
     const bool vec = (p.ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0;
-    float sm[4];
-    float4 sg[NJ], su[SWIGLU ? NJ : 1];
-    if constexpr (OUT != 2) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm[i] = p.s[min(mrow + 16 * i, p.M - 1)];
-        const int cmax = (SWIGLU ? ncols : p.Np) - 4;  // scales hold Np entries
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int c = min(cbase + 16 * j, cmax);
-            sg[j] = *reinterpret_cast<const float4*>(p.wscale + c);
-            if constexpr (SWIGLU) su[j] = *reinterpret_cast<const float4*>(p.wscale + (p.N >> 1) + c);
-        }
-        // stores share the in-order memory counter with loads: wait for the scales
-        // once here so no store below waits behind another
-        wait_all_memory();
-    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = mrow + 16 * i;
