@@ -293,6 +293,16 @@ __device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float 
     }
 }
 
+// Brings the parameters a workgroup's prologue needs into scalar registers at once.
+// Left to itself the compiler fetches them field by field as the code reaches them, and
+// reuses their registers, so the prologue waited on 4-5 kernel-argument loads in series
+// before its first global load; an empty asm that reads them all makes it issue the loads
+// together and wait once.
+__device__ __forceinline__ void gemv_fetch_params(const GemvParams& p) {
+    asm volatile("" ::"s"(p.W), "s"(p.wscale), "s"(p.wrow), "s"(p.K), "s"(p.Kp), "s"(p.N), "s"(p.M), "s"(p.A),
+                 "s"(p.lda), "s"(p.flags), "s"(p.grid), "s"(p.iw));
+}
+
 // MODE 0: q/s given.  MODE 1: fused quant of fp16 rows.  MODE 2: fused quant of f32 rows.
 // MR: largest row count of the fused modes (1 or 4).  NORM: RMSNorm before the
 // quantization (fused modes, one row).
@@ -307,6 +317,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
+    gemv_fetch_params(p);
     __shared__ float s_inv[kFusedMaxRows];
     __shared__ float s_red[WAVES][kFusedMaxRows];
     __shared__ int s_bad[WAVES];
@@ -563,6 +574,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
+    gemv_fetch_params(p);
     __shared__ float s_inv[kFusedMaxRows];
     __shared__ float s_red[WAVES][kFusedMaxRows];
     __shared__ int s_bad[WAVES];
