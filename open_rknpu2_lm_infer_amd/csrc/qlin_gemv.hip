@@ -319,7 +319,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     __shared__ float s_rows[kGemvMaxRows];
     gemv_fetch_params(p);
     __shared__ float s_inv[kFusedMaxRows];
-    __shared__ float s_red[WAVES][kFusedMaxRows];
+    __shared__ float s_red[kFusedMaxRows][WAVES];  // wave maxima per row (0 from waves owning no group)
     __shared__ int s_bad[WAVES];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -451,24 +451,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
-                if (m < p.M) {
-                    const float w = wave_max_nonneg(mx[m]);
-                    if (lane == 0) s_red[wave][m] = w;
-                }
+            for (int m = 0; m < MR; ++m) {
+                const float w = m < p.M ? wave_max_nonneg(mx[m]) : 0.0f;
+                if (lane == 0) s_red[m][wave] = w;
+            }
             const bool any_bad = __ballot(bad) != 0;
             if (lane == 0) s_bad[wave] = any_bad;
+        } else if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) s_red[m][wave] = 0.0f;
+            s_bad[wave] = 0;
         }
         lds_barrier();
-        // per-token scales, computed by every thread from the wave maxima
-        const int owners = min(WAVES, (ngroups + 63) / 64);
+        // Per-token scales, computed by every thread from all WAVES wave maxima (zeros,
+        // the identity of a max of magnitudes, from the waves that own no group): a loop
+        // of fixed length lets the reads issue back to back and wait once; one bounded by
+        // the number of owning waves waited for each read in turn (about 1 us per launch).
         int bad_rows = 0;
-        for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
         float inv[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             float am = 0.0f;
-            for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
             const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
             inv[m] = 1.0f / s;
             if (tid == 0 && m < p.M) s_rows[m] = s;
@@ -576,7 +583,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     __shared__ float s_rows[kGemvMaxRows];
     gemv_fetch_params(p);
     __shared__ float s_inv[kFusedMaxRows];
-    __shared__ float s_red[WAVES][kFusedMaxRows];
+    __shared__ float s_red[kFusedMaxRows][WAVES];  // wave maxima per row (0 from waves owning no group)
     __shared__ int s_bad[WAVES];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -727,24 +734,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
-                if (m < p.M) {
-                    const float w = wave_max_nonneg(mx[m]);
-                    if (lane == 0) s_red[wave][m] = w;
-                }
+            for (int m = 0; m < MR; ++m) {
+                const float w = m < p.M ? wave_max_nonneg(mx[m]) : 0.0f;
+                if (lane == 0) s_red[m][wave] = w;
+            }
             const bool any_bad = __ballot(bad) != 0;
             if (lane == 0) s_bad[wave] = any_bad;
+        } else if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) s_red[m][wave] = 0.0f;
+            s_bad[wave] = 0;
         }
         lds_barrier();
-        // per-token scales, computed by every thread from the wave maxima
-        const int owners = min(WAVES, (ngroups + 63) / 64);
+        // Per-token scales, computed by every thread from all WAVES wave maxima (zeros,
+        // the identity of a max of magnitudes, from the waves that own no group): a loop
+        // of fixed length lets the reads issue back to back and wait once; one bounded by
+        // the number of owning waves waited for each read in turn (about 1 us per launch).
         int bad_rows = 0;
-        for (int w = 0; w < owners; ++w) bad_rows |= s_bad[w];
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
         float inv[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             float am = 0.0f;
-            for (int w = 0; w < owners; ++w) am = fmaxf(am, s_red[w][m]);
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
             const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
             inv[m] = 1.0f / s;
             if (tid == 0 && m < p.M) s_rows[m] = s;
