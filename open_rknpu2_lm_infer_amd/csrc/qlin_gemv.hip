@@ -463,56 +463,60 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             s_bad[wave] = 0;
         }
         lds_barrier();
-        // Per-token scales, computed by every thread from all WAVES wave maxima (zeros,
-        // the identity of a max of magnitudes, from the waves that own no group): a loop
-        // of fixed length lets the reads issue back to back and wait once; one bounded by
-        // the number of owning waves waited for each read in turn (about 1 us per launch).
-        int bad_rows = 0;
+        // Per-token scales, computed by every thread of the waves that hold activation
+        // groups (the others go straight to the barrier instead of spending the SIMDs on
+        // scales they do not use) from all WAVES wave maxima (zeros, the identity of a max
+        // of magnitudes, from the waves that own no group): a loop of fixed length lets
+        // the reads issue back to back and wait once; one bounded by the number of owning
+        // waves waited for each read in turn (about 1 us per launch).
+        if (owner_wave) {
+            int bad_rows = 0;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
-        float inv[MR];
+            for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
+            float inv[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float am = 0.0f;
+            for (int m = 0; m < MR; ++m) {
+                float am = 0.0f;
 #pragma unroll
-            for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
-            const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
-            inv[m] = 1.0f / s;
-            if (tid == 0 && m < p.M) s_rows[m] = s;
-        }
-        if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
-        if (owner_wave && !bad_rows) {
-            // finite rows (the usual case): the short rounding sequence
-            if (rne)
-                gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
-            else
-                gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
-        } else if (owner_wave) {
+                for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
+                const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+                inv[m] = 1.0f / s;
+                if (tid == 0 && m < p.M) s_rows[m] = s;
+            }
+            if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+            if (!bad_rows) {
+                // finite rows (the usual case): the short rounding sequence
+                if (rne)
+                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                else
+                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+            } else {
 #pragma unroll
-            for (int i = 0; i < XR; ++i) {
-                if (i < nreg) {
-                    const int m = i / gpt, g = tid + NT * (i - m * gpt);
-                    if (g < ngroups) {
-                        float v[8];
-                        xr[i].get(v);
-                        if constexpr (NORM) {
+                for (int i = 0; i < XR; ++i) {
+                    if (i < nreg) {
+                        const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                        if (g < ngroups) {
+                            float v[8];
+                            xr[i].get(v);
+                            if constexpr (NORM) {
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                            }
+                            float im = 1.0f;
+#pragma unroll
+                            for (int mm = 0; mm < MR; ++mm)
+                                if (mm == m) im = inv[mm];
+                            int q[8];
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+                            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                            }
+                            *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                         }
-                        float im = 1.0f;
-#pragma unroll
-                        for (int mm = 0; mm < MR; ++mm)
-                            if (mm == m) im = inv[mm];
-                        int q[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
-                        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-                        }
-                        *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                     }
                 }
             }
@@ -746,56 +750,60 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             s_bad[wave] = 0;
         }
         lds_barrier();
-        // Per-token scales, computed by every thread from all WAVES wave maxima (zeros,
-        // the identity of a max of magnitudes, from the waves that own no group): a loop
-        // of fixed length lets the reads issue back to back and wait once; one bounded by
-        // the number of owning waves waited for each read in turn (about 1 us per launch).
-        int bad_rows = 0;
+        // Per-token scales, computed by every thread of the waves that hold activation
+        // groups (the others go straight to the barrier instead of spending the SIMDs on
+        // scales they do not use) from all WAVES wave maxima (zeros, the identity of a max
+        // of magnitudes, from the waves that own no group): a loop of fixed length lets
+        // the reads issue back to back and wait once; one bounded by the number of owning
+        // waves waited for each read in turn (about 1 us per launch).
+        if (owner_wave) {
+            int bad_rows = 0;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
-        float inv[MR];
+            for (int w = 0; w < WAVES; ++w) bad_rows |= s_bad[w];
+            float inv[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float am = 0.0f;
+            for (int m = 0; m < MR; ++m) {
+                float am = 0.0f;
 #pragma unroll
-            for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
-            const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
-            inv[m] = 1.0f / s;
-            if (tid == 0 && m < p.M) s_rows[m] = s;
-        }
-        if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
-        if (owner_wave && !bad_rows) {
-            // finite rows (the usual case): the short rounding sequence
-            if (rne)
-                gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
-            else
-                gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
-        } else if (owner_wave) {
+                for (int w = 0; w < WAVES; ++w) am = fmaxf(am, s_red[m][w]);
+                const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+                inv[m] = 1.0f / s;
+                if (tid == 0 && m < p.M) s_rows[m] = s;
+            }
+            if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+            if (!bad_rows) {
+                // finite rows (the usual case): the short rounding sequence
+                if (rne)
+                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                else
+                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+            } else {
 #pragma unroll
-            for (int i = 0; i < XR; ++i) {
-                if (i < nreg) {
-                    const int m = i / gpt, g = tid + NT * (i - m * gpt);
-                    if (g < ngroups) {
-                        float v[8];
-                        xr[i].get(v);
-                        if constexpr (NORM) {
+                for (int i = 0; i < XR; ++i) {
+                    if (i < nreg) {
+                        const int m = i / gpt, g = tid + NT * (i - m * gpt);
+                        if (g < ngroups) {
+                            float v[8];
+                            xr[i].get(v);
+                            if constexpr (NORM) {
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                            }
+                            float im = 1.0f;
+#pragma unroll
+                            for (int mm = 0; mm < MR; ++mm)
+                                if (mm == m) im = inv[mm];
+                            int q[8];
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+                            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                                w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                            }
+                            *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                         }
-                        float im = 1.0f;
-#pragma unroll
-                        for (int mm = 0; mm < MR; ++mm)
-                            if (mm == m) im = inv[mm];
-                        int q[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
-                        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-                            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-                        }
-                        *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
                     }
                 }
             }
