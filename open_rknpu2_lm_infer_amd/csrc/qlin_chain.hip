@@ -352,7 +352,7 @@ __device__ int chain_stage(const ChainParams& p, const ChainStage& st, int s, ui
                 if constexpr (SWIGLU) {
                     const int a_u = BITS == 4 ? (vu >> 4) : vu;
                     const float up = ((float)a_u * s_rows[m]) * st.wscale[Nh + cg];
-                    o = (o / (1.0f + expf(-o))) * up;  // src/npu.rs:1202-1208
+                    o = silu_gate(o, up);  // src/npu.rs:1202-1208
                 }
                 const _Float16 h = f16_of_f32(o);
                 __hip_atomic_store(reinterpret_cast<uint16_t*>(out) + (int64_t)m * ld_out + cg,

@@ -417,7 +417,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
                         int au = acc[i][j + NJ][r];
                         if (BITS == 4) au >>= 4;
                         const float u = ((float)au * sm[i]) * su[j][r];
-                        o[r] = (g / (1.0f + expf(-g))) * u;
+                        o[r] = silu_gate(g, u);  // src/npu.rs:1202-1208
                     } else {
                         o[r] = g;
                     }

@@ -218,7 +218,7 @@ __device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, in
     if constexpr (SWIGLU) {
         const int au = BITS == 4 ? (vu >> 4) : vu;
         const float up = ((float)au * sm) * wsu;  // wsu = wscale[N/2 + cg]
-        out = (out / (1.0f + expf(-out))) * up;  // src/npu.rs:1202-1208
+        out = silu_gate(out, up);  // src/npu.rs:1202-1208
     }
     if (cg < (SWIGLU ? Nh : p.N)) {
         if (p.c_kind == 1)

@@ -155,6 +155,17 @@ __device__ __forceinline__ float f32_of_f16_bits(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
+// SiLU(g) * u (src/npu.rs:1202-1208: g / (1 + e^-g) * u) with the hardware exp2 and
+// reciprocal: e^-g = exp2(-g * log2 e), then g * rcp(1 + e^-g).  v_exp_f32 and v_rcp_f32
+// are accurate to about 1 ulp, so the result stays within a few ulp of the IEEE
+// expression, far inside the SwiGLU tolerance; this is 4 instructions where expf and the
+// correctly rounded divide took about 30.  For g < -88, e^-g is +inf and the result is
+// -0 * u, as in the IEEE form.
+__device__ __forceinline__ float silu_gate(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
+
 // fp16 store of an f32 result, rounded twice as specified (to f32 by the producing
 // operation, then to fp16 to nearest even).  The empty asm pins x in a VGPR as a
 // rounded f32 value; without it the backend folds the producing multiply into
