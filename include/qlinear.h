@@ -49,6 +49,7 @@ extern "C" {
                                      16-accumulator order of src/model/cpu.rs:11-41 */
 #define QLIN_SWIGLU 0x4u          /* fused SiLU(gate)*up epilogue, output [M, N/2] */
 #define QLIN_NO_FUSED_QUANT 0x8u  /* decode: quantize in a separate launch instead of in the GEMV */
+#define QLIN_RESIDUAL 0x10u       /* chain stage: add a residual row after the linear (see qlin_chain_stage) */
 
 typedef struct qlin_weights qlin_weights;
 typedef struct qlin_workspace qlin_workspace;
@@ -178,6 +179,18 @@ int qlin_run_rmsnorm(qlin_workspace* ws, const qlin_weights* weights, int32_t ro
                      const void* A, int32_t a_dtype, int64_t lda, const float* gamma, float eps,
                      void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream);
 
+/* Linear, then the decoder's residual update in the same epilogue (src/model/dense.rs:478-489
+ * and 528-537: Projection::run, Cpu::scale(projected, residual_multiplier), Cpu::add(hidden,
+ * projected)):  C[m,n] = R[m,n] + y[m,n] * multiplier, where y is what qlin_run computes, every
+ * operation an f32 rounding (the add in the reference's order hidden + projected, add_chunk in
+ * src/model/cpu.rs:68-85), then stored as c_dtype.  R: device [rows, ldr] of r_dtype (f32 or
+ * fp16); R may equal C with ldr == ldc (the in-place hidden += of the reference).  Not with
+ * QLIN_SWIGLU (QLIN_ERR_PARAM).  No counterpart in the native library: the reference runs the
+ * scale and add on the CPU after rk_npu_w4a8_run_f32 / rk_npu_f32i8f32_run_dynamic return. */
+int qlin_run_residual(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, const void* A,
+                      int32_t a_dtype, int64_t lda, const void* R, int32_t r_dtype, int64_t ldr,
+                      float multiplier, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream);
+
 /* ---- stage entry points (parity checks and composition) ----
  * Per-token quantization alone (the library's scan + quantize,
  * QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:26-27).  q: device int8 [rows, ldq], the
@@ -221,10 +234,11 @@ int qlin_tune_load(const char* path);
  * (Cpu::norm, then Projection::run / run_swiglu for qkv, o, gate_up, down, layer
  * after layer).  Each stage computes exactly what qlin_run_rmsnorm (gamma != NULL)
  * or qlin_run (gamma == NULL) computes for its input, with fp16 in and out: the
- * chain output equals those calls made one after another.  Attention, RoPE and the
- * residual adds are not part of it; a stage reads an earlier stage's output (or the
- * chain input) from a column offset, so a caller can route e.g. the q columns of qkv
- * into o. */
+ * chain output equals those calls made one after another.  Attention and RoPE are not
+ * part of it; a stage reads an earlier stage's output (or the chain input) from a column
+ * offset, so a caller can route e.g. the q columns of qkv into o.  A stage with
+ * QLIN_RESIDUAL computes what qlin_run_residual computes, with R = an earlier stage's
+ * output or the chain input (the decoder's hidden += o(...) and hidden += down(...)). */
 typedef struct qlin_chain qlin_chain;
 
 typedef struct qlin_chain_stage {
@@ -234,6 +248,10 @@ typedef struct qlin_chain_stage {
     float eps;
     int32_t input;        /* -1: the chain input; j >= 0: the output of stage j (j < this) */
     int32_t input_offset; /* first column taken from that output (multiple of 8) */
+    /* with QLIN_RESIDUAL in flags (not with QLIN_SWIGLU): */
+    int32_t residual;     /* -1: the chain input; j >= 0: the output of stage j (j < this) */
+    int32_t residual_offset;   /* first column of the residual rows (multiple of 8) */
+    float residual_multiplier; /* the linear's output is scaled by this before the add */
 } qlin_chain_stage;
 
 /* Checks the stages (K of each stage = the columns it reads; K % 8 == 0) and

@@ -28,6 +28,7 @@ QLIN_ROUND_HALF_EVEN = 0x1
 QLIN_NORM_SEQUENTIAL = 0x2
 QLIN_SWIGLU = 0x4
 QLIN_NO_FUSED_QUANT = 0x8
+QLIN_RESIDUAL = 0x10
 
 QLIN_PACK_QUANTIZED = 0
 QLIN_INT_QUANTIZED = 1
@@ -54,6 +55,8 @@ SIGNATURES = {
     "qlin_run_swiglu_f32": (ctypes.c_int, [_P, _P, _I32, _P, _P]),
     "qlin_run": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I64, _P, _I32, _I64, _U32, _P]),
     "qlin_run_rmsnorm": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I64, _P, _F, _P, _I32, _I64, _U32, _P]),
+    "qlin_run_residual": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I64, _P, _I32, _I64, _F, _P, _I32, _I64, _U32,
+                                         _P]),
     "qlin_quantize": (ctypes.c_int, [_I32, _I32, _P, _I32, _I64, _P, _F, _P, _I64, _P, _P, _U32, _P]),
     "qlin_gemm_i32": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _I64, _P]),
     "qlin_run_quantized": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _P, _I32, _I64, _U32, _P]),
@@ -92,7 +95,8 @@ class DeviceInfo(ctypes.Structure):
 
 class ChainStage(ctypes.Structure):
     _fields_ = [("weights", _P), ("flags", _U32), ("gamma", _P), ("eps", _F), ("input", _I32),
-                ("input_offset", _I32)]
+                ("input_offset", _I32), ("residual", _I32), ("residual_offset", _I32),
+                ("residual_multiplier", _F)]
 
 
 class QlinError(RuntimeError):

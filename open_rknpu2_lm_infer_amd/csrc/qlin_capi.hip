@@ -488,6 +488,14 @@ namespace {
 
 // Output channels per GEMV item: QLIN_GEMV_ITEM_WIDTH (1..16) if set, else the width in
 // 8..16 that spreads the items most evenly over the CUs.
+// Residual update of the epilogue (qlin_run_residual, chain stages with QLIN_RESIDUAL).
+struct ResidualArgs {
+    const void* R;
+    int64_t ldr;
+    int r_f16;
+    float mult;
+};
+
 int gemv_width(const qlin_weights* w, bool sw, int cus) {
     const int forced = env_int("QLIN_GEMV_ITEM_WIDTH", 0);
     if (forced >= 1 && forced <= 16) return forced;
@@ -496,9 +504,15 @@ int gemv_width(const qlin_weights* w, bool sw, int cus) {
 
 int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
              const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
-             int64_t ldc, uint32_t flags, hipStream_t st) {
+             int64_t ldc, uint32_t flags, hipStream_t st, const ResidualArgs* res = nullptr) {
     const bool sw = (flags & kFlagSwiglu) != 0;
     GemvParams p{};
+    if (res) {
+        p.R = res->R;
+        p.ldr = res->ldr;
+        p.r_f16 = res->r_f16;
+        p.rmult = res->mult;
+    }
     p.W = w->W;
     p.wscale = w->scales;
     p.wrow = w->wrow;
@@ -557,9 +571,15 @@ bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, c
 }
 
 int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* q, int64_t ldq, const float* s,
-             void* C, int c_kind, int64_t ldc, uint32_t flags, hipStream_t st) {
+             void* C, int c_kind, int64_t ldc, uint32_t flags, hipStream_t st, const ResidualArgs* res = nullptr) {
     const bool sw = (flags & kFlagSwiglu) != 0;
     GemmParams p{};
+    if (res) {
+        p.R = res->R;
+        p.ldr = res->ldr;
+        p.r_f16 = res->r_f16;
+        p.rmult = res->mult;
+    }
     p.W = w->W;
     p.wscale = w->scales;
     p.wrow = w->wrow;
@@ -617,7 +637,8 @@ int check_run(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
 }
 
 int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_dtype, int64_t lda,
-             const float* gamma, float eps, void* C, int c_dtype, int64_t ldc, uint32_t flags, hipStream_t st) {
+             const float* gamma, float eps, void* C, int c_dtype, int64_t ldc, uint32_t flags, hipStream_t st,
+             const ResidualArgs* res = nullptr) {
     if (int rc = check_run(ws, w, rows, flags)) return rc;
     if (!A || !C || lda < w->K || (a_dtype != QLIN_F32 && a_dtype != QLIN_F16) ||
         (c_dtype != QLIN_F32 && c_dtype != QLIN_F16))
@@ -628,7 +649,7 @@ int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     ws->last = st;
     if (gemv_fusable(w, rows, A, lda, gamma, flags)) {
         return run_gemv(ws, w, rows, A, a_dtype == QLIN_F16, lda, gamma, eps, nullptr, 0, nullptr, C,
-                        c_dtype == QLIN_F16, ldc, flags, st);
+                        c_dtype == QLIN_F16, ldc, flags, st, res);
     }
     QuantParams qp{};
     qp.A = A;
@@ -645,8 +666,8 @@ int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     if (launch_quant(qp, rows, st) != hipSuccess) return QLIN_ERR_DEVICE;
     if (gemv_ok(ws, w, rows))
         return run_gemv(ws, w, rows, nullptr, 0, 0, nullptr, 0.0f, ws->q, w->Kp, ws->s, C, c_dtype == QLIN_F16,
-                        ldc, flags, st);
-    return run_gemm(ws, w, rows, ws->q, w->Kp, ws->s, C, c_dtype == QLIN_F16 ? 1 : 0, ldc, flags, st);
+                        ldc, flags, st, res);
+    return run_gemm(ws, w, rows, ws->q, w->Kp, ws->s, C, c_dtype == QLIN_F16 ? 1 : 0, ldc, flags, st, res);
 }
 
 int run_host(qlin_workspace* ws, const qlin_weights* w, int rows, const float* A, float* C, uint32_t flags) {
@@ -691,6 +712,18 @@ int qlin_run_rmsnorm(qlin_workspace* ws, const qlin_weights* w, int32_t rows, co
                      uint32_t flags, void* stream) {
     if (!gamma) return QLIN_ERR_PARAM;
     return run_impl(ws, w, rows, A, a_dtype, lda, gamma, eps, C, c_dtype, ldc, flags, (hipStream_t)stream);
+}
+
+int qlin_run_residual(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const void* A, int32_t a_dtype,
+                      int64_t lda, const void* R, int32_t r_dtype, int64_t ldr, float multiplier, void* C,
+                      int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream) {
+    if (!w || (flags & kFlagSwiglu) || !R || (r_dtype != QLIN_F32 && r_dtype != QLIN_F16) || ldr < w->N ||
+        !std::isfinite(multiplier))
+        return QLIN_ERR_PARAM;
+    // in place (the reference's hidden += projected) only element for element
+    if (R == C && (ldr != ldc || r_dtype != c_dtype)) return QLIN_ERR_PARAM;
+    const ResidualArgs res{R, ldr, r_dtype == QLIN_F16 ? 1 : 0, multiplier};
+    return run_impl(ws, w, rows, A, a_dtype, lda, nullptr, 0.0f, C, c_dtype, ldc, flags, (hipStream_t)stream, &res);
 }
 
 int qlin_gemm_i32(qlin_workspace* ws, const qlin_weights* w, int32_t rows, const int8_t* q, int64_t ldq,
@@ -767,7 +800,7 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
     c->cols.resize(n);
     c->outs.assign(n, nullptr);
     c->ld.assign(n, 0);
-    const uint32_t allowed = QLIN_SWIGLU | QLIN_ROUND_HALF_EVEN | QLIN_NORM_SEQUENTIAL;
+    const uint32_t allowed = QLIN_SWIGLU | QLIN_ROUND_HALF_EVEN | QLIN_NORM_SEQUENTIAL | QLIN_RESIDUAL;
     int rc = QLIN_OK;
     for (int s = 0; s < n && rc == QLIN_OK; ++s) {
         const qlin_chain_stage& d = st[s];
@@ -786,6 +819,15 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
             break;
         }
         c->cols[s] = (d.flags & QLIN_SWIGLU) ? w->N / 2 : w->N;
+        if (d.flags & QLIN_RESIDUAL) {
+            if ((d.flags & QLIN_SWIGLU) || d.residual < -1 || d.residual >= s || d.residual_offset < 0 ||
+                d.residual_offset % 8 || !std::isfinite(d.residual_multiplier) ||
+                (d.residual >= 0 && d.residual_offset + c->cols[s] > c->cols[d.residual])) {
+                rc = QLIN_ERR_PARAM;
+                break;
+            }
+            if (d.residual == -1) c->x_cols = std::max(c->x_cols, d.residual_offset + c->cols[s]);
+        }
         if (d.input == -1) {
             c->x_cols = std::max(c->x_cols, d.input_offset + w->K);
         } else if (d.input_offset + w->K > c->cols[d.input]) {
@@ -806,6 +848,9 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
         cs.gamma = d.gamma;
         cs.eps = d.eps;
         cs.x_offset = d.input == -1 ? d.input_offset : 0;
+        cs.res_kind = (d.flags & QLIN_RESIDUAL) ? (d.residual == -1 ? 1 : 2) : 0;
+        cs.res_x_offset = cs.res_kind == 1 ? d.residual_offset : 0;
+        cs.rmult = d.residual_multiplier;
         c->kp_max = std::max(c->kp_max, w->Kp);
         c->k_max = std::max(c->k_max, w->K);
     }
@@ -828,6 +873,10 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
         cs.ld_in = in >= 0 ? c->ld[in] : 0;
         cs.out = c->outs[s];
         cs.ld_out = c->ld[s];
+        if (cs.res_kind == 2) {
+            cs.res = reinterpret_cast<const __half*>(c->outs[st[s].residual]) + st[s].residual_offset;
+            cs.ld_res = c->ld[st[s].residual];
+        }
     }
     if (rc == QLIN_OK &&
         (hipMalloc(&c->d_stages, sizeof(ChainStage) * n) != hipSuccess ||

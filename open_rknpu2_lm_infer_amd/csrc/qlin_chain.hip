@@ -353,6 +353,19 @@ __device__ int chain_stage(const ChainParams& p, const ChainStage& st, int s, ui
                     const int a_u = BITS == 4 ? (vu >> 4) : vu;
                     const float up = ((float)a_u * s_rows[m]) * st.wscale[Nh + cg];
                     o = silu_gate(o, up);  // src/npu.rs:1202-1208
+                } else if (st.res_kind) {
+                    // src/model/dense.rs:486-489: hidden + projected * residual_multiplier; an
+                    // earlier stage's rows are read device-coherently like a stage input
+                    const float pr = o * st.rmult;
+                    float hv;
+                    if (st.res_kind == 1) {
+                        hv = __half2float(p.x[(int64_t)m * p.ldx + st.res_x_offset + cg]);
+                    } else {
+                        const uint16_t bits = __hip_atomic_load(reinterpret_cast<const uint16_t*>(st.res) + (int64_t)m * st.ld_res + cg,
+                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        hv = (float)__builtin_bit_cast(_Float16, bits);
+                    }
+                    o = hv + pr;
                 }
                 const _Float16 h = f16_of_f32(o);
                 __hip_atomic_store(reinterpret_cast<uint16_t*>(out) + (int64_t)m * ld_out + cg,

@@ -21,6 +21,13 @@ struct ChainStage {
     int x_offset;           // first chain-input column read (when in is null)
     _Float16* out;          // stage output rows [rows, N or N/2]
     int64_t ld_out;
+    // residual update (res_kind 1: the chain input from column res_x_offset; 2: an earlier
+    // stage's output at res): out = R + y * rmult
+    int res_kind;
+    const __half* res;
+    int64_t ld_res;
+    int res_x_offset;
+    float rmult;
 };
 
 struct ChainParams {

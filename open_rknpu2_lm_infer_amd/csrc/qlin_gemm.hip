@@ -422,6 +422,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
                         o[r] = g;
                     }
                 }
+                if (!SWIGLU && p.R) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)  // src/model/dense.rs:486-489
+                        if (c + r < ncols) o[r] = residual_add(p.R, p.ldr, p.r_f16, p.rmult, m, c + r, o[r]);
+                }
                 if constexpr (OUT == 1) {
                     _Float16* C = reinterpret_cast<_Float16*>(p.C) + at;
                     if (vec && c + 3 < ncols) {

@@ -221,6 +221,7 @@ __device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int n, in
         out = silu_gate(out, up);  // src/npu.rs:1202-1208
     }
     if (cg < (SWIGLU ? Nh : p.N)) {
+        if (!SWIGLU && p.R) out = residual_add(p.R, p.ldr, p.r_f16, p.rmult, m, cg, out);  // src/model/dense.rs:486-489
         if (p.c_kind == 1)
             reinterpret_cast<_Float16*>(p.C)[(int64_t)m * p.ldc + cg] = f16_of_f32(out);
         else

@@ -67,6 +67,11 @@ struct GemvParams {
     int grid;           // workgroups (each takes items b, b + grid, ...); 0: one per item
     int iw;             // output channels per item, 1..16 (the MFMA tile's 16 rows; rows past
                         // iw re-read the item's last row and are not stored)
+    // residual update of the epilogue (R != null): C = R + y * rmult, f32 roundings
+    const void* R;
+    int64_t ldr;
+    int r_f16;
+    float rmult;
 };
 
 // Items of a GEMV launch: output channels (N, or N/2 with SwiGLU) in groups of iw.
@@ -94,7 +99,23 @@ struct GemmParams {
     int32_t* part;        // split-K partials, tile-major
     uint32_t* counters;   // [m_tiles * n_tiles], zero at rest
     int deep;             // 1: the most LDS stages (grid of at most one workgroup per CU)
+    // residual update of the epilogue (R != null): C = R + y * rmult, f32 roundings
+    const void* R;
+    int64_t ldr;
+    int r_f16;
+    float rmult;
 };
+
+// Residual update of an f32 epilogue value y at (m, c): R[m, c] + y * mult, each an f32
+// rounding, the add in the reference's order hidden + projected (src/model/dense.rs:486-489,
+// src/model/cpu.rs:68-85).  x * 1 is exact, so a multiplier of one equals the reference's
+// skipped scale.
+__device__ __forceinline__ float residual_add(const void* R, int64_t ldr, int r_f16, float mult, int m, int c, float y) {
+    const float p = y * mult;
+    const float h = r_f16 ? (float)reinterpret_cast<const _Float16*>(R)[(int64_t)m * ldr + c]
+                          : reinterpret_cast<const float*>(R)[(int64_t)m * ldr + c];
+    return h + p;
+}
 
 // Launchers (return hipError_t of the launch).
 hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream);

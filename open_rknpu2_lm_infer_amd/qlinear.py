@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 from ._lib import (QLIN_F16, QLIN_F32, QLIN_NO_FUSED_QUANT, QLIN_NORM_SEQUENTIAL,  # noqa: F401
-                   QLIN_ROUND_HALF_EVEN, QLIN_SWIGLU, check)
+                   QLIN_RESIDUAL, QLIN_ROUND_HALF_EVEN, QLIN_SWIGLU, check)
 
 _DT = {torch.float32: QLIN_F32, torch.float16: QLIN_F16}
 
@@ -109,15 +109,21 @@ class Chain:
     """Decode chain (qlin_chain): several linears in one persistent launch, 1..4 rows of
     fp16 activations.  stages: dicts with weights (Weights), flags, gamma (device f32
     [K] or None), eps, input (-1 = chain input, j = output of stage j; default: the
-    previous stage) and offset (first column read)."""
+    previous stage), offset (first column read) and, for a residual stage, residual
+    (-1 = chain input, j = output of stage j), residual_offset and residual_scale
+    (QLIN_RESIDUAL is added to the flags when residual is given)."""
 
     def __init__(self, stages: list, max_rows: int = 1):
         arr = (_lib.ChainStage * len(stages))()
         self._keep = []
         for i, st in enumerate(stages):
             g = st.get("gamma")
-            arr[i] = _lib.ChainStage(st["weights"].handle, st.get("flags", 0), g.data_ptr() if g is not None else None,
-                                     st.get("eps", 1e-6), st.get("input", -1 if i == 0 else i - 1), st.get("offset", 0))
+            res = st.get("residual")
+            flags = st.get("flags", 0) | (QLIN_RESIDUAL if res is not None else 0)
+            arr[i] = _lib.ChainStage(st["weights"].handle, flags, g.data_ptr() if g is not None else None,
+                                     st.get("eps", 1e-6), st.get("input", -1 if i == 0 else i - 1), st.get("offset", 0),
+                                     res if res is not None else 0, st.get("residual_offset", 0),
+                                     st.get("residual_scale", 1.0))
             self._keep.append(st["weights"])
             if g is not None:
                 self._keep.append(g)
@@ -185,14 +191,22 @@ def tune_load(path: str) -> int:
 
 def run(ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor | None = None,
         out_dtype=torch.float16, flags: int = 0, gamma: torch.Tensor | None = None,
-        eps: float = 1e-6) -> torch.Tensor:
-    """out[M, N] (or [M, N/2] with QLIN_SWIGLU) = quantized linear of A[M, K] (device)."""
+        eps: float = 1e-6, residual: torch.Tensor | None = None, residual_scale: float = 1.0) -> torch.Tensor:
+    """out[M, N] (or [M, N/2] with QLIN_SWIGLU) = quantized linear of A[M, K] (device).
+    With residual R [M, N]: out = R + linear * residual_scale (qlin_run_residual; out may be R)."""
     M = A.shape[0]
     ncols = w.N // 2 if flags & QLIN_SWIGLU else w.N
     if out is None:
         out = torch.empty((M, ncols), dtype=out_dtype, device=A.device)
     assert A.stride(1) == 1 and out.stride(1) == 1
     L = _lib.load()
+    if residual is not None:
+        assert gamma is None and residual.stride(1) == 1
+        rc = L.qlin_run_residual(ws.handle, w.handle, M, _ptr(A), _DT[A.dtype], A.stride(0), _ptr(residual),
+                                 _DT[residual.dtype], residual.stride(0), residual_scale, _ptr(out), _DT[out.dtype],
+                                 out.stride(0), flags, _stream())
+        check(rc, "qlin_run_residual")
+        return out
     if gamma is None:
         rc = L.qlin_run(ws.handle, w.handle, M, _ptr(A), _DT[A.dtype], A.stride(0), _ptr(out), _DT[out.dtype],
                         out.stride(0), flags, _stream())

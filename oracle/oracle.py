@@ -45,6 +45,7 @@ def lib():
             "oracle_gemm_i32_digit_split": (None, [P, I, I, I, P, I, P]),
             "oracle_dequant": (None, [P, I, I, P, P, P]),
             "oracle_swiglu": (None, [P, I, I, P]),
+            "oracle_residual_add": (None, [P, P, I, I, F]),
             "oracle_rmsnorm_neon16": (None, [P, I, I, I, P, F, P]),
             "oracle_rmsnorm_seq": (None, [P, I, I, I, P, F, P]),
             "oracle_f32_to_f16_array": (None, [P, I, P]),
@@ -120,6 +121,15 @@ def dequant(acc, s, scales):
     out = np.zeros((M, N), np.float32)
     lib().oracle_dequant(_p(acc), M, N, _p(s), _p(scales), _p(out))
     return out
+
+
+def residual_add(hidden, projected, multiplier=1.0):
+    """hidden + projected * multiplier (f32, the decoder's residual update); returns a new array."""
+    h = np.array(hidden, dtype=np.float32, copy=True, order="C")
+    pr = np.ascontiguousarray(projected, dtype=np.float32)
+    M, N = h.shape
+    lib().oracle_residual_add(_p(h), _p(pr), M, N, multiplier)
+    return h
 
 
 def swiglu(out):

@@ -114,6 +114,16 @@ void oracle_dequant(const int32_t* acc, int64_t M, int64_t N, const float* s, co
         for (int64_t n = 0; n < N; ++n) out[m * N + n] = ((float)acc[m * N + n] * s[m]) * scales[n];
 }
 
+/* src/model/dense.rs:486-489: scale (skipped at 1.0, src/model/cpu.rs:247-253), then
+ * add_chunk's y[i] += x[i] (src/model/cpu.rs:68-85) */
+void oracle_residual_add(float* hidden, const float* projected, int64_t M, int64_t N, float multiplier) {
+    for (int64_t i = 0; i < M * N; ++i) {
+        float p = projected[i];
+        if (multiplier != 1.0f) p = p * multiplier;
+        hidden[i] = hidden[i] + p;
+    }
+}
+
 /* src/npu.rs:1202-1208 */
 void oracle_swiglu(const float* out, int64_t M, int64_t N, float* mid) {
     int64_t F = N / 2;

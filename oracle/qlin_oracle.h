@@ -59,6 +59,11 @@ void oracle_gemm_i32_digit_split(const int8_t* q, int64_t ldq, int64_t M, int64_
 void oracle_dequant(const int32_t* acc, int64_t M, int64_t N, const float* s, const float* scales,
                     float* out);
 
+/* src/model/dense.rs:486-489 and 534-537 (Cpu::scale then Cpu::add, src/model/cpu.rs:68-85,
+ * 237-253): hidden[m,n] = hidden[m,n] + projected[m,n]*multiplier, in place, each an f32
+ * rounding; Cpu::scale skips a multiplier of exactly 1 (x*1 == x, so the same result). */
+void oracle_residual_add(float* hidden, const float* projected, int64_t M, int64_t N, float multiplier);
+
 /* src/npu.rs:1202-1208 / src/model/cpu.rs:119-152: mid[m,j] = (g/(1+exp(-g)))*u
  * with g = out[m,j], u = out[m,j+N/2]; mid is [M, N/2]. */
 void oracle_swiglu(const float* out, int64_t M, int64_t N, float* mid);

@@ -90,3 +90,4 @@ def test_structs_match_header_sizes():
     assert ctypes.sizeof(_lib.WeightInfo) == 32
     assert ctypes.sizeof(_lib.WorkspaceInfo) == 24
     assert ctypes.sizeof(_lib.DeviceInfo) == 48
+    assert ctypes.sizeof(_lib.ChainStage) == 48

@@ -142,6 +142,32 @@ def test_swiglu_against_float64(oracle):
     assert mid[0, 0] == 0.0 or abs(mid[0, 0]) < 1e-30
 
 
+def test_residual_add_roundings(oracle):
+    """hidden + projected * m as two f32 roundings in the reference's order
+    (src/model/dense.rs:486-489): known answers that a fused multiply-add, a dropped
+    multiplier or a wrong rounding would each fail."""
+    h = np.array([[1.0, 1.0, 3.0]], np.float32)
+    p = np.array([[2.0**-24, 2.0**-24 + 2.0**-47, 1.0]], np.float32)
+    out = oracle.residual_add(h, p, 1.0)
+    assert out[0, 0] == 1.0  # 1 + 2^-24 is a tie: to even
+    assert out[0, 1] == np.float32(1 + 2.0**-23)
+    assert out[0, 2] == 4.0
+    # (1 + 2^-23)^2 = 1 + 2^-22 + 2^-46 rounds to 1 + 2^-22 before the add, so the sum is
+    # exactly 0; one rounding (an FMA) would leave 2^-46
+    m = float(np.float32(1 + 2.0**-23))
+    out = oracle.residual_add(np.array([[-(1 + 2.0**-22)]], np.float32), np.array([[m]], np.float32), m)
+    assert out[0, 0] == 0.0
+    rng = np.random.default_rng(11)
+    hid = rng.standard_normal((4, 64)).astype(np.float32)
+    pr = rng.standard_normal((4, 64)).astype(np.float32)
+    assert np.array_equal(oracle.residual_add(hid, pr, 0.0), hid)  # multiplier 0: hidden unchanged
+    assert np.array_equal(oracle.residual_add(np.zeros_like(pr), pr, 1.0), pr)
+    # the input arrays are not modified
+    h0 = hid.copy()
+    oracle.residual_add(hid, pr, 0.5)
+    assert np.array_equal(hid, h0)
+
+
 # ---------------------------------------------------------------- RMSNorm
 
 
