@@ -208,4 +208,97 @@ void Linear::run_device(const void* A, int a_dtype, int64_t lda, void* C, int c_
           "device run");
 }
 
+QuantMatrix concatenate(std::vector<QuantMatrix> matrices) {
+    ensure(!matrices.empty(), "empty fused projection");
+    if (matrices.size() == 1) return std::move(matrices[0]);
+    const uint32_t bits = matrices[0].bits;
+    const size_t k = matrices[0].k;
+    for (const QuantMatrix& m : matrices)
+        ensure(m.bits == bits && m.k == k, "fused projections require identical bit widths and K");
+    QuantMatrix out;
+    out.bits = bits;
+    out.k = k;
+    for (const QuantMatrix& m : matrices) {
+        out.n += m.n;
+        out.scales.insert(out.scales.end(), m.scales.begin(), m.scales.end());
+    }
+    out.codes.resize(k * out.n);
+    for (size_t ki = 0; ki < k; ++ki) {  // K-major rows: each row is the modules' rows side by side
+        size_t offset = 0;
+        for (const QuantMatrix& m : matrices) {
+            std::copy(m.codes.begin() + ki * m.n, m.codes.begin() + (ki + 1) * m.n, out.codes.begin() + ki * out.n + offset);
+            offset += m.n;
+        }
+    }
+    return out;
+}
+
+Projection Projection::load(Backend& backend, std::vector<QuantMatrix> modules) {
+    Projection result;
+    size_t first = 0;
+    while (first < modules.size()) {
+        const uint32_t bits = modules[first].bits;
+        size_t last = first + 1;
+        while (last < modules.size() && modules[last].bits == bits) ++last;
+        std::vector<QuantMatrix> group;
+        for (size_t i = first; i < last; ++i) group.push_back(std::move(modules[i]));
+        Linear linear = backend.load(concatenate(std::move(group)));
+        const size_t n = linear.n();
+        result.parts_.emplace_back(std::move(linear), result.width_);
+        result.width_ += n;
+        first = last;
+    }
+    return result;
+}
+
+size_t Projection::scratch_width() const {
+    if (parts_.size() <= 1) return 0;
+    size_t w = 0;
+    for (const auto& p : parts_) w = std::max(w, p.first.n());
+    return w;
+}
+
+void Projection::run(const float* input, size_t input_len, float* output, size_t output_len, size_t rows,
+                     float* scratch, size_t scratch_len) const {
+    run_from(0, input, input_len, output, output_len, rows, scratch, scratch_len);
+}
+
+void Projection::run_from(size_t first, const float* input, size_t input_len, float* output, size_t output_len,
+                          size_t rows, float* scratch, size_t scratch_len) const {
+    ensure(first < parts_.size(), "invalid projection suffix");
+    const size_t base = parts_[first].second;
+    const size_t width = width_ - base;
+    ensure(output_len == rows * width, "projection suffix shape mismatch");
+    if (parts_.size() - first == 1) {
+        parts_[first].first.run(input, input_len, output, output_len, rows);
+        return;
+    }
+    for (size_t i = first; i < parts_.size(); ++i) {
+        const Linear& linear = parts_[i].first;
+        const size_t offset = parts_[i].second - base, n = linear.n();
+        if (rows == 1) {
+            linear.run(input, input_len, output + offset, n, 1);
+        } else {
+            ensure(scratch && scratch_len >= rows * n, "projection scratch too small");
+            linear.run(input, input_len, scratch, rows * n, rows);
+            for (size_t r = 0; r < rows; ++r)
+                std::copy(scratch + r * n, scratch + (r + 1) * n, output + r * width + offset);
+        }
+    }
+}
+
+bool Projection::run_swiglu(const float* input, size_t input_len, float* output, size_t output_len,
+                            size_t rows) const {
+    if (parts_.size() != 1) return false;
+    return parts_[0].first.run_swiglu(input, input_len, output, output_len, rows);
+}
+
+void Projection::run_device(const void* A, int a_dtype, int64_t lda, void* C, int c_dtype, int64_t ldc, size_t rows,
+                            void* stream) const {
+    ensure(ldc >= (int64_t)width_, "projection output stride below its width");
+    const size_t elem = c_dtype == QLIN_F16 ? 2 : 4;
+    for (const auto& p : parts_)
+        p.first.run_device(A, a_dtype, lda, static_cast<uint8_t*>(C) + p.second * elem, c_dtype, ldc, rows, 0, stream);
+}
+
 }  // namespace npu

@@ -91,4 +91,36 @@ public:
     std::shared_ptr<State> state;
 };
 
+// src/model/checkpoint.rs:392-423: modules joined along N in order (same bits and K).
+QuantMatrix concatenate(std::vector<QuantMatrix> matrices);
+
+// The quantized Projection of src/model/projection.rs:110-243: one Linear per run of
+// consecutive same-bit modules (each run concatenated along N), outputs side by side in
+// module order in rows of width() columns.
+class Projection {
+public:
+    // src/model/projection.rs:141-188: modules in module order (e.g. q, k, v).
+    static Projection load(Backend& backend, std::vector<QuantMatrix> modules);
+    size_t width() const { return width_; }
+    size_t parts() const { return parts_.size(); }
+    size_t scratch_width() const;  // src/model/projection.rs:130-140
+    // src/model/projection.rs:190-232: input f32 [rows, K]; output f32 [rows, width of the
+    // suffix from part `first`]; scratch f32 [rows * scratch_width()] (unused at one row or
+    // with one part).
+    void run(const float* input, size_t input_len, float* output, size_t output_len, size_t rows,
+             float* scratch, size_t scratch_len) const;
+    void run_from(size_t first, const float* input, size_t input_len, float* output, size_t output_len, size_t rows,
+                  float* scratch, size_t scratch_len) const;
+    // src/model/projection.rs:233-243: fused only with a single part.
+    bool run_swiglu(const float* input, size_t input_len, float* output, size_t output_len, size_t rows) const;
+    // Device rows: every part writes its own columns of C [rows, ldc >= width()] directly
+    // (no scratch copy); asynchronous on `stream`.
+    void run_device(const void* A, int a_dtype, int64_t lda, void* C, int c_dtype, int64_t ldc, size_t rows,
+                    void* stream) const;
+
+private:
+    std::vector<std::pair<Linear, size_t>> parts_;  // (linear, first output column)
+    size_t width_ = 0;
+};
+
 }  // namespace npu

@@ -2,6 +2,8 @@
 // through the npu::Backend / npu::Linear mirror:
 //   quantized_linear_padding_and_swiglu       src/npu.rs:1161-1224
 //   narrow_w8_gdn_gates_match_integer_oracle  src/npu/narrow_projection.rs:3-68
+// plus the mixed-bit Projection (src/model/projection.rs:110-243) and concatenate
+// (src/model/checkpoint.rs:392-423) of the mirror.
 // Inputs are the tests' own closed forms; the checker is the CPU oracle
 // (oracle/qlin_oracle.c) at the tests' own tolerances, plus bit-equality of the
 // f32 outputs (both sides do the same singly-rounded f32 operations).
@@ -90,7 +92,67 @@ static int cpu_tests() {
         backend.load(npu::QuantMatrix{4, 4, 4, std::vector<int8_t>(16), std::vector<float>(3, 1.0f)});
     });
     EXPECT(backend.tune_operations() == 0, "tune operations");
+    // concatenate (src/model/checkpoint.rs:392-423): K-major rows side by side, scales in order
+    {
+        npu::QuantMatrix a{8, 2, 2, {1, 2, 3, 4}, {0.5f, 0.25f}}, b{8, 2, 1, {9, 8}, {2.0f}};
+        const npu::QuantMatrix c = npu::concatenate({a, b});
+        const std::vector<int8_t> codes{1, 2, 9, 3, 4, 8};
+        const std::vector<float> scales{0.5f, 0.25f, 2.0f};
+        EXPECT(c.bits == 8 && c.k == 2 && c.n == 3 && c.codes == codes && c.scales == scales, "concatenate");
+        expect_error("fused projections require identical bit widths and K", [&] {
+            npu::concatenate({a, npu::QuantMatrix{4, 2, 1, {1, 2}, {1.0f}}});
+        });
+        expect_error("empty fused projection", [] { npu::concatenate({}); });
+    }
     return failures;
+}
+
+// Projection of q (W4), k and v (W8): two parts (the W4 run, then k and v fused along N),
+// outputs side by side; each module's columns equal the oracle of that module alone.
+static void projection_tests(npu::Backend& backend) {
+    const size_t K = 256, nq = 96, nk = 32, nv = 32;
+    auto module = [&](uint32_t bits, size_t n, int salt) {
+        npu::QuantMatrix m;
+        m.bits = bits;
+        m.k = K;
+        m.n = n;
+        const int lo = bits == 4 ? -8 : -127, span = bits == 4 ? 16 : 255;
+        for (size_t i = 0; i < K * n; ++i) m.codes.push_back((int8_t)((long)(i * 29 + salt * 7 + i / n) % span + lo));
+        for (size_t i = 0; i < n; ++i) m.scales.push_back(0.003f + (float)((i + salt) % 13) * 0.0007f);
+        return m;
+    };
+    const std::vector<npu::QuantMatrix> mods{module(4, nq, 1), module(8, nk, 2), module(8, nv, 3)};
+    npu::Projection proj = npu::Projection::load(backend, mods);
+    EXPECT(proj.parts() == 2 && proj.width() == nq + nk + nv, "projection parts %zu width %zu", proj.parts(), proj.width());
+    EXPECT(proj.scratch_width() == nq, "scratch width %zu", proj.scratch_width());
+    for (size_t rows : {1u, 3u}) {
+        std::vector<float> input(rows * K);
+        for (size_t i = 0; i < input.size(); ++i) input[i] = (float)((i * 31 + 7) % 113) / 37.0f - 1.5f;
+        std::vector<float> out(rows * proj.width()), scratch(rows * proj.scratch_width());
+        proj.run(input.data(), input.size(), out.data(), out.size(), rows, scratch.data(), scratch.size());
+        size_t col = 0;
+        for (const npu::QuantMatrix& m : mods) {
+            const std::vector<float> ref = reference_oracle(m, input, rows);
+            for (size_t r = 0; r < rows; ++r)
+                EXPECT(std::memcmp(out.data() + r * proj.width() + col, ref.data() + r * m.n, m.n * sizeof(float)) == 0,
+                       "projection rows %zu: columns %zu.. differ from the module alone", rows, col);
+            col += m.n;
+        }
+        // run_from(1): the k, v suffix only (src/model/projection.rs:198-232)
+        std::vector<float> kv(rows * (nk + nv));
+        proj.run_from(1, input.data(), input.size(), kv.data(), kv.size(), rows, scratch.data(), scratch.size());
+        for (size_t r = 0; r < rows; ++r)
+            EXPECT(std::memcmp(kv.data() + r * (nk + nv), out.data() + r * proj.width() + nq, (nk + nv) * sizeof(float)) == 0,
+                   "run_from(1) rows %zu", rows);
+        std::vector<float> mid(rows * proj.width() / 2);
+        EXPECT(!proj.run_swiglu(input.data(), input.size(), mid.data(), mid.size(), rows), "two parts fused a SwiGLU");
+        expect_error("projection suffix shape mismatch", [&] {
+            proj.run_from(1, input.data(), input.size(), kv.data(), kv.size() - 1, rows, scratch.data(), scratch.size());
+        });
+        expect_error("invalid projection suffix", [&] {
+            proj.run_from(2, input.data(), input.size(), kv.data(), kv.size(), rows, scratch.data(), scratch.size());
+        });
+    }
 }
 
 static npu::QuantMatrix padding_matrix(uint32_t bits) {
@@ -134,6 +196,7 @@ static int gpu_tests() {
             }
         }
     }
+    projection_tests(backend);
     // src/npu.rs:1213-1222: workspaces are bounded by retain_workspaces, no tuning at run time
     backend.retain_workspaces({1, 64});
     EXPECT(backend.stats().find("\"workspace_count\": 1") != std::string::npos ||
