@@ -108,6 +108,25 @@ def test_rmsnorm_quantize_bitexact(oracle, order, M, K):
     assert np.array_equal(q.cpu().numpy()[:, :K], qo)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("order", ["neon16", "seq"])
+@pytest.mark.parametrize("M,K", [(1027, 2560), (1030, 104), (1025, 9728)])
+def test_rmsnorm_quantize_many_rows(oracle, dtype, order, M, K):
+    """Many rows take the one-wave-per-row staged kernel (64-thread workgroups)."""
+    x = synth.activations(M, K, seed=K + M, device="cpu", dist="student_t3").to(dtype)
+    gam = synth.gamma(K, seed=K, device="cpu")
+    flags = ql.QLIN_NORM_SEQUENTIAL if order == "seq" else 0
+    ldq = roundup(K, 256)
+    q, s = ql.quantize(x.to(DEV), ldq=ldq, gamma=gam.to(DEV), eps=1e-6, flags=flags)
+    torch.cuda.synchronize()
+    y = oracle.rmsnorm(x.float().numpy(), gam.numpy(), 1e-6, order)
+    qo, so, _ = oracle.quantize(y)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    qh = q.cpu().numpy()
+    assert np.array_equal(qh[:, :K], qo)
+    assert not qh[:, K:].any()  # the zero tail up to ldq
+
+
 # ------------------------------------------------------------------ integer accumulators
 
 
