@@ -625,6 +625,7 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     // a grid with at most one workgroup per CU takes the deeper pipeline
     const int deep_env = env_int("QLIN_GEMM_DEEP", -1);
     p.deep = deep_env >= 0 ? (deep_env != 0) : (int64_t)tiles * p.splits <= ws->cu_count;
+    p.wn = env_int("QLIN_GEMM_WN", 4) == 2 ? 2 : 4;  // 2 x 4 waves unless QLIN_GEMM_WN=2
     return launch_gemm(p, w->bits, bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 

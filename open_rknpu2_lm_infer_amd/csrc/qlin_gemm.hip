@@ -3,8 +3,12 @@
 // int32 reduce (QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:28-31); gfx950 multiplies
 // the int8 codes directly, so no digit split or correction term is needed.
 //
-// Tile 128 (rows) x BN (channels) x 128 (k); 256 threads as 2 x 2 waves,
-// each wave 64 x BN/2 = 4 x BN/32 tiles of v_mfma_i32_16x16x64_i8 per 64-k half.
+// Tile 128 (rows) x BN (channels) x 128 (k); 128 * WN threads as 2 x WN waves, each
+// wave 64 x BN/WN = 4 x BN/(16 WN) tiles of v_mfma_i32_16x16x64_i8 per 64-k half.
+// WN = 4 (512 threads, the default) puts two waves on every SIMD even when a CU holds
+// one workgroup: one wave's LDS reads and W4 unpack overlap the other's MFMAs (M = 512
+// qkv 23.2 -> 20.9 us, the four layer linears 122.6 -> 114.5 us).  WN = 2 is the 2 x 2
+// layout with 64 x 64 per wave (a quarter fewer LDS reads per MFMA, one wave per SIMD).
 //
 // Operands go from global memory straight into LDS (buffer_load_dwordx4 ... lds):
 // one instruction fills 1 KiB of LDS in lane order, and which global 16-byte chunk a
@@ -42,22 +46,27 @@
 namespace qlin {
 
 constexpr int BM = 128, BK = 128;
-constexpr int kGemmThreads = 256;
 constexpr int kLdsBytes = 160 * 1024;  // LDS of one gfx950 CU
 
 // W4 stages are 24 KiB: three of them let two workgroups share a CU, so one's MFMAs
 // run while the other waits on LDS.  W8 stages are 32 KiB: one workgroup, four stages.
-template <int BITS, int BN, int NSTAGES = (BITS == 4 ? 3 : 4)>
+// WN: waves along N (2 x WN waves of 64 rows x BN / WN channels each).  WN = 4 puts two
+// waves on every SIMD when the grid holds one workgroup per CU, so one wave's LDS reads
+// and unpack overlap the other's MFMAs (a quarter more LDS reads per MFMA).
+template <int BITS, int BN, int NSTAGES = (BITS == 4 ? 3 : 4), int WN = 2>
 struct GemmGeom {
-    static constexpr int NI = BN / 32;                         // B fragments per wave
+    static constexpr int THREADS = 128 * WN;
+    static constexpr int NI = BN / (16 * WN);                  // B fragments per wave
     static constexpr int A_BYTES = BM * BK;                    // 16 KiB
     static constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;      // bytes of one B row
     static constexpr int B_BYTES = BN * B_ROW;
     static constexpr int STAGE = A_BYTES + B_BYTES;
     static constexpr int NST = kLdsBytes / STAGE < NSTAGES ? kLdsBytes / STAGE : NSTAGES;  // stages
     static constexpr int LDS = NST * STAGE;
-    static constexpr int NA = A_BYTES / 1024 / 4;              // 1 KiB copies per wave per stage
-    static constexpr int NB = B_BYTES / 1024 / 4;
+    static constexpr int NA = A_BYTES / 1024 / (2 * WN);       // 1 KiB copies per wave per stage
+    static constexpr int NB = B_BYTES / 1024 / (2 * WN);
+    static_assert(NA >= 1 && NB >= 1 && NA * 1024 * 2 * WN == A_BYTES && NB * 1024 * 2 * WN == B_BYTES,
+                  "copy plan");
     static constexpr int NL = NA + NB;
     static constexpr int REGS = 4 * NI * 4;                    // int32 accumulators per lane
     static_assert(NST >= 3, "pipeline needs three LDS stages");
@@ -108,18 +117,18 @@ __device__ __forceinline__ v4i unpack_w4(int x, int y) {
                (int)(uy & 0xF0F0F0F0u)};
 }
 
-template <bool SWIGLU, int BN>
+template <bool SWIGLU, int BN, int WN>
 __device__ __forceinline__ constexpr int b_frag_row(int wn, int j) {
-    constexpr int NI = BN / 32;
-    if constexpr (SWIGLU) return (j >= NI / 2 ? BN / 2 : 0) + wn * (BN / 4) + (j % (NI / 2)) * 16;
-    return wn * (BN / 2) + j * 16;
+    constexpr int NI = BN / (16 * WN);
+    if constexpr (SWIGLU) return (j >= NI / 2 ? BN / 2 : 0) + wn * (BN / (2 * WN)) + (j % (NI / 2)) * 16;
+    return wn * (BN / WN) + j * 16;
 }
 
 // Global -> LDS copy plan of one wave: NA activation blocks of 8 rows x 128 bytes and
 // NB weight blocks (W8: 8 rows x 128 bytes; W4: 16 rows x 64 bytes).
-template <int BITS, bool SWIGLU, int BN>
+template <int BITS, bool SWIGLU, int BN, int WN>
 struct Copy {
-    using G = GemmGeom<BITS, BN>;
+    using G = GemmGeom<BITS, BN, 3, WN>;
     __amdgpu_buffer_rsrc_t ra, rg, ru;
     int aoff[G::NA], boff[G::NB];
     int wave;
@@ -172,21 +181,21 @@ struct Copy {
 };
 
 // Fragment registers of one k tile: packed or int8 weight fragments for both halves.
-template <int BITS, int BN>
+template <int BITS, int BN, int WN>
 struct BFrag {
-    v4i v[BITS == 4 ? BN / 32 : 2 * (BN / 32)];
+    v4i v[BITS == 4 ? BN / (16 * WN) : 2 * (BN / (16 * WN))];
 };
 
-template <int BITS, bool SWIGLU, int BN>
-__device__ __forceinline__ void read_b(BFrag<BITS, BN>& b, const uint8_t* sb, int bbase0, int bbase1, int wn) {
-    constexpr int NI = BN / 32;
+template <int BITS, bool SWIGLU, int BN, int WN>
+__device__ __forceinline__ void read_b(BFrag<BITS, BN, WN>& b, const uint8_t* sb, int bbase0, int bbase1, int wn) {
+    constexpr int NI = BN / (16 * WN);
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         if constexpr (BITS == 4) {
-            b.v[j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN>(wn, j) * 64);
+            b.v[j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN, WN>(wn, j) * 64);
         } else {
-            b.v[2 * j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN>(wn, j) * 128);
-            b.v[2 * j + 1] = *reinterpret_cast<const v4i*>(sb + bbase1 + b_frag_row<SWIGLU, BN>(wn, j) * 128);
+            b.v[2 * j] = *reinterpret_cast<const v4i*>(sb + bbase0 + b_frag_row<SWIGLU, BN, WN>(wn, j) * 128);
+            b.v[2 * j + 1] = *reinterpret_cast<const v4i*>(sb + bbase1 + b_frag_row<SWIGLU, BN, WN>(wn, j) * 128);
         }
     }
 }
@@ -196,9 +205,10 @@ __device__ __forceinline__ void read_a(v4i (&a)[4], const uint8_t* sa, int abase
     for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4i*>(sa + abase + i * 16 * 128);
 }
 
-template <int BITS, int BN>
-__device__ __forceinline__ void mma_half(v4i (&acc)[4][BN / 32], const v4i (&a)[4], const BFrag<BITS, BN>& b, int h) {
-    constexpr int NI = BN / 32;
+template <int BITS, int BN, int WN>
+__device__ __forceinline__ void mma_half(v4i (&acc)[4][BN / (16 * WN)], const v4i (&a)[4], const BFrag<BITS, BN, WN>& b,
+                                         int h) {
+    constexpr int NI = BN / (16 * WN);
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         const v4i w = BITS == 4 ? (h == 0 ? unpack_w4(b.v[j][0], b.v[j][1]) : unpack_w4(b.v[j][2], b.v[j][3]))
@@ -233,16 +243,17 @@ __device__ __forceinline__ void order_region() {
 // One k tile: multiply tile t (its first-half A fragments in a0, B in bc); read its
 // second-half A fragments, then, after the barrier, the next tile's first-half A and
 // its B fragments into bn.
-template <int BITS, bool SWIGLU, int BN, int NSTG>
-__device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], v4i (&a1)[4], const BFrag<BITS, BN>& bc,
-                                          BFrag<BITS, BN>& bn, const Copy<BITS, SWIGLU, BN>& cp, uint8_t* smem, int t,
-                                          int kt_begin, int last, int abase0, int abase1, int bbase0, int bbase1, int wn) {
-    using G = GemmGeom<BITS, BN, NSTG>;
+template <int BITS, bool SWIGLU, int BN, int NSTG, int WN>
+__device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / (16 * WN)], v4i (&a0)[4], v4i (&a1)[4],
+                                          const BFrag<BITS, BN, WN>& bc, BFrag<BITS, BN, WN>& bn,
+                                          const Copy<BITS, SWIGLU, BN, WN>& cp, uint8_t* smem, int t, int kt_begin,
+                                          int last, int abase0, int abase1, int bbase0, int bbase1, int wn) {
+    using G = GemmGeom<BITS, BN, NSTG, WN>;
     constexpr int NREAD_B = BITS == 4 ? G::NI : 2 * G::NI;     // 16-byte B reads per tile
     constexpr int VPJ = BITS == 4 ? 6 : 0;                     // unpack VALU work per B fragment
     const uint8_t* s0 = smem + (t % G::NST) * G::STAGE;
     read_a(a1, s0, abase1);
-    mma_half<BITS, BN>(acc, a0, bc, 0);
+    mma_half<BITS, BN, WN>(acc, a0, bc, 0);
     order_region<G::NI, VPJ, 4, 0>();
     // Nothing moves across the two fences below: each half's MFMAs then use fragments
     // read one half (16 MFMAs) earlier instead of waiting on reads just issued.
@@ -258,19 +269,19 @@ __device__ __forceinline__ void gemm_step(v4i (&acc)[4][BN / 32], v4i (&a0)[4], 
     cp.issue(smem, (fill % G::NST) * G::STAGE, min(kt_begin + fill, last));
     const uint8_t* s1 = smem + ((t + 1) % G::NST) * G::STAGE;
     read_a(a0, s1, abase0);
-    read_b<BITS, SWIGLU, BN>(bn, s1 + G::A_BYTES, bbase0, bbase1, wn);
-    mma_half<BITS, BN>(acc, a1, bc, 1);
+    read_b<BITS, SWIGLU, BN, WN>(bn, s1 + G::A_BYTES, bbase0, bbase1, wn);
+    mma_half<BITS, BN, WN>(acc, a1, bc, 1);
     order_region<G::NI, VPJ, 4 + NREAD_B, G::NL>();
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
-    using G = GemmGeom<BITS, BN, NSTG>;
+template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG, int WN>
+__global__ __launch_bounds__(128 * WN) void gemm_kernel(GemmParams p) {
+    using G = GemmGeom<BITS, BN, NSTG, WN>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int fr = lane & 15, fc = lane >> 4;
 
     const int tiles = p.m_tiles * p.n_tiles;
@@ -313,7 +324,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     // retire before the first copy wait, which counts only copies issued after them.)
     constexpr int NJ = SWIGLU ? G::NI / 2 : G::NI;
     const int mrow = m0 + wm * 64 + fr;
-    const int cbase = n0 + wn * (SWIGLU ? BN / 4 : BN / 2) + 4 * fc;
+    const int cbase = n0 + wn * (SWIGLU ? BN / (2 * WN) : BN / WN) + 4 * fc;
     const int ncols = SWIGLU ? (p.N >> 1) : p.N;
     float sm[4];
     float4 sg[NJ], su[SWIGLU ? NJ : 1];
@@ -330,22 +341,22 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     }
 
     {
-        const Copy<BITS, SWIGLU, BN> cp(p, m0, n0, wave, lane);
+        const Copy<BITS, SWIGLU, BN, WN> cp(p, m0, n0, wave, lane);
 #pragma unroll
         for (int s = 0; s < G::NST - 1; ++s) cp.issue(smem, s * G::STAGE, min(kt_begin + s, last));
         wait_vm<(G::NST - 2) * G::NL>();
         barrier_no_fence();
 
         v4i a0[4], a1[4];
-        BFrag<BITS, BN> bx, by;
+        BFrag<BITS, BN, WN> bx, by;
         read_a(a0, smem, abase0);
-        read_b<BITS, SWIGLU, BN>(bx, smem + G::A_BYTES, bbase0, bbase1, wn);
+        read_b<BITS, SWIGLU, BN, WN>(bx, smem + G::A_BYTES, bbase0, bbase1, wn);
 
         for (int t = 0; t < T; t += 2) {
-            gemm_step<BITS, SWIGLU, BN, NSTG>(acc, a0, a1, bx, by, cp, smem, t, kt_begin, last, abase0, abase1, bbase0,
-                                              bbase1, wn);
-            gemm_step<BITS, SWIGLU, BN, NSTG>(acc, a0, a1, by, bx, cp, smem, t + 1, kt_begin, last, abase0, abase1,
-                                              bbase0, bbase1, wn);
+            gemm_step<BITS, SWIGLU, BN, NSTG, WN>(acc, a0, a1, bx, by, cp, smem, t, kt_begin, last, abase0, abase1,
+                                                  bbase0, bbase1, wn);
+            gemm_step<BITS, SWIGLU, BN, NSTG, WN>(acc, a0, a1, by, bx, cp, smem, t + 1, kt_begin, last, abase0, abase1,
+                                                  bbase0, bbase1, wn);
         }
         // drain the surplus copies before the LDS is reused or the workgroup ends
         wait_vm<0>();
@@ -353,15 +364,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     }
 
     if (p.splits > 1) {
-        const int64_t base = (int64_t)tile * p.splits * G::REGS * kGemmThreads;
-        int32_t* mine = p.part + base + (int64_t)z * G::REGS * kGemmThreads;
+        const int64_t base = (int64_t)tile * p.splits * G::REGS * G::THREADS;
+        int32_t* mine = p.part + base + (int64_t)z * G::REGS * G::THREADS;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < G::NI; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    store_coherent(mine + ((i * G::NI + j) * 4 + r) * kGemmThreads + tid, acc[i][j][r]);
+                    store_coherent(mine + ((i * G::NI + j) * 4 + r) * G::THREADS + tid, acc[i][j][r]);
         wait_all_memory();
         __syncthreads();
         int* flag = reinterpret_cast<int*>(smem);  // the LDS stages are drained
@@ -370,14 +381,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
         if (!flag[0]) return;
         for (int zz = 0; zz < p.splits; ++zz) {
             if (zz == z) continue;
-            const int32_t* other = p.part + base + (int64_t)zz * G::REGS * kGemmThreads;
+            const int32_t* other = p.part + base + (int64_t)zz * G::REGS * G::THREADS;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < G::NI; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += load_coherent(other + ((i * G::NI + j) * 4 + r) * kGemmThreads + tid);
+                        acc[i][j][r] += load_coherent(other + ((i * G::NI + j) * 4 + r) * G::THREADS + tid);
         }
         if (tid == 0) atomicExch(&p.counters[tile], 0u);
     }
@@ -455,15 +466,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmParams p) {
     }
 }
 
-template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG>
+template <int BITS, bool SWIGLU, int OUT, int BN, int NSTG, int WN>
 static hipError_t launch_gemm_s(const GemmParams& p, hipStream_t stream) {
-    using G = GemmGeom<BITS, BN, NSTG>;
+    using G = GemmGeom<BITS, BN, NSTG, WN>;
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG>),
+        reinterpret_cast<const void*>(&gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG, WN>),
         hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (attr != hipSuccess) return attr;
-    dim3 grid(p.m_tiles * p.n_tiles * p.splits), block(kGemmThreads);
-    gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG><<<grid, block, G::LDS, stream>>>(p);
+    dim3 grid(p.m_tiles * p.n_tiles * p.splits), block(G::THREADS);
+    gemm_kernel<BITS, SWIGLU, OUT, BN, NSTG, WN><<<grid, block, G::LDS, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -473,8 +484,12 @@ static hipError_t launch_gemm_s(const GemmParams& p, hipStream_t stream) {
 template <int BITS, bool SWIGLU, int OUT, int BN>
 static hipError_t launch_gemm_t(const GemmParams& p, hipStream_t stream) {
     constexpr int DEEP = BITS == 4 ? 6 : 4;
-    if (p.deep) return launch_gemm_s<BITS, SWIGLU, OUT, BN, DEEP>(p, stream);
-    return launch_gemm_s<BITS, SWIGLU, OUT, BN, (BITS == 4 ? 3 : 4)>(p, stream);
+    if (p.deep) {
+        if (p.wn == 4) return launch_gemm_s<BITS, SWIGLU, OUT, BN, DEEP, 4>(p, stream);
+        return launch_gemm_s<BITS, SWIGLU, OUT, BN, DEEP, 2>(p, stream);
+    }
+    if (p.wn == 4) return launch_gemm_s<BITS, SWIGLU, OUT, BN, (BITS == 4 ? 3 : 4), 4>(p, stream);
+    return launch_gemm_s<BITS, SWIGLU, OUT, BN, (BITS == 4 ? 3 : 4), 2>(p, stream);
 }
 
 template <int BITS, int BN>

@@ -99,6 +99,7 @@ struct GemmParams {
     int32_t* part;        // split-K partials, tile-major
     uint32_t* counters;   // [m_tiles * n_tiles], zero at rest
     int deep;             // 1: the most LDS stages (grid of at most one workgroup per CU)
+    int wn;               // waves along N: 4 (2 x 4 waves, two per SIMD at one workgroup per CU) or 2
     // residual update of the epilogue (R != null): C = R + y * rmult, f32 roundings
     const void* R;
     int64_t ldr;
