@@ -47,6 +47,9 @@ struct GemvCfg {
     static constexpr int XREGS = WAVES >= 16 ? 2 : 8;
 };
 constexpr int fused_regs(int waves) { return waves >= 16 ? 2 : 8; }
+// Several rows with RMSNorm hold gamma per register slot as well: fewer slots keep the
+// prologue within the register file.
+constexpr int kNormRowsRegs = 4;
 
 // LDS of gemv_items_kernel: the quantized rows (and the f32 rows of the RMSNorm before
 // them), then the partial-sum area [items][gate, up][WAVES][lanes][regs].
@@ -261,8 +264,8 @@ struct XGroup<float> {
 
 // Quantized rows of the fused prologue into LDS for finite rows (quant_finite).
 template <int BITS, bool NORM, bool RNE, int MR, int XR, typename XG>
-__device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float (&gr)[NORM ? XR : 1][8], float nscale,
-                                                const float (&inv)[MR], uint8_t* lds_a, int astride, int nreg, int gpt,
+__device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float (&gr)[NORM ? XR : 1][8],
+                                                const float (&nsc)[MR], const float (&inv)[MR], uint8_t* lds_a, int astride, int nreg, int gpt,
                                                 int ngroups, int tid, int NT) {
 #pragma unroll
     for (int i = 0; i < XR; ++i) {
@@ -272,8 +275,12 @@ __device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float 
                 float v[8];
                 xr[i].get(v);
                 if constexpr (NORM) {
+                    float ns = 1.0f;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                    for (int mm = 0; mm < MR; ++mm)
+                        if (mm == m) ns = nsc[mm];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
                 }
                 float im = 1.0f;
 #pragma unroll
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = NORM && MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -357,10 +364,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             }
         }
         if constexpr (NORM) {
+            // gamma for every held group (rows share it: one copy per register slot keeps
+            // the indexing static)
 #pragma unroll
             for (int i = 0; i < XR; ++i) {
-                const int g = tid + NT * i;
-                if (i < gpt && g < ngroups) {
+                const int m = MR == 1 ? 0 : i / gpt, g = tid + NT * (i - m * gpt);
+                if (i < nreg && g < ngroups) {
                     const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
                     const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
                     gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
@@ -389,29 +398,34 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     uint8_t* lds_a = smem;
     if constexpr (FUSED) {
         const bool rne = (p.flags & kFlagRne) != 0;
-        float nscale = 1.0f;
+        float nsc[MR];  // RMSNorm scale per row
+#pragma unroll
+        for (int m = 0; m < MR; ++m) nsc[m] = 1.0f;
         if constexpr (NORM) {
-            // the reference summation order needs the whole row in one place
+            // the reference summation order needs each whole row in one place: f32 rows
+            // [M][K] in LDS, one wave per row
             float* lds_x = reinterpret_cast<float*>(smem);
 #pragma unroll
             for (int i = 0; i < XR; ++i) {
-                const int g = tid + NT * i;
-                if (i < gpt && g < ngroups) {
+                const int m = MR == 1 ? 0 : i / gpt, g = tid + NT * (i - m * gpt);
+                if (i < nreg && g < ngroups) {
                     float v[8];
                     xr[i].get(v);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) lds_x[8 * g + e] = v[e];
+                    for (int e = 0; e < 8; ++e) lds_x[m * p.K + 8 * g + e] = v[e];
                 }
             }
             lds_barrier();
-            if (tid < 64) {
-                const float sum = (p.flags & kFlagNormSeq) != 0 ? (tid == 0 ? lds_sumsq_seq(lds_x, p.K) : 0.0f)  // src/ops/norm.rs:38
-                                                                : lds_sumsq_neon16(lds_x, p.K);  // src/model/cpu.rs:14-35
-                if (tid == 0) s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+            if (wave < p.M) {
+                const float* xm = lds_x + wave * p.K;
+                const float sum = (p.flags & kFlagNormSeq) != 0 ? (lane == 0 ? lds_sumsq_seq(xm, p.K) : 0.0f)  // src/ops/norm.rs:38
+                                                                : lds_sumsq_neon16(xm, p.K);  // src/model/cpu.rs:14-35
+                if (lane == 0) s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
             }
             lds_barrier();
-            nscale = s_inv[0];
-            lds_barrier();  // lds_x is overwritten by the quantized row below
+#pragma unroll
+            for (int m = 0; m < MR; ++m) nsc[m] = m < p.M ? s_inv[m] : 1.0f;
+            lds_barrier();  // lds_x is overwritten by the quantized rows below
         }
         const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
         if (owner_wave) {
@@ -437,8 +451,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 #pragma unroll
                             for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
                             if constexpr (NORM) {
+                                float ns = 1.0f;
 #pragma unroll
-                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int mm = 0; mm < MR; ++mm)
+                                    if (mm == m) ns = nsc[mm];
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
                             }
                             lm = 0.0f;
 #pragma unroll
@@ -488,9 +506,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             if (!bad_rows) {
                 // finite rows (the usual case): the short rounding sequence
                 if (rne)
-                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
                 else
-                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
             } else {
 #pragma unroll
                 for (int i = 0; i < XR; ++i) {
@@ -500,8 +518,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                             float v[8];
                             xr[i].get(v);
                             if constexpr (NORM) {
+                                float ns = 1.0f;
 #pragma unroll
-                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int mm = 0; mm < MR; ++mm)
+                                    if (mm == m) ns = nsc[mm];
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
                             }
                             float im = 1.0f;
 #pragma unroll
@@ -582,7 +604,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = NORM && MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -630,10 +652,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             }
         }
         if constexpr (NORM) {
+            // gamma for every held group (rows share it: one copy per register slot keeps
+            // the indexing static)
 #pragma unroll
             for (int i = 0; i < XR; ++i) {
-                const int g = tid + NT * i;
-                if (i < gpt && g < ngroups) {
+                const int m = MR == 1 ? 0 : i / gpt, g = tid + NT * (i - m * gpt);
+                if (i < nreg && g < ngroups) {
                     const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
                     const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
                     gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
@@ -676,29 +700,34 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     uint8_t* lds_a = smem;
     if constexpr (FUSED) {
         const bool rne = (p.flags & kFlagRne) != 0;
-        float nscale = 1.0f;
+        float nsc[MR];  // RMSNorm scale per row
+#pragma unroll
+        for (int m = 0; m < MR; ++m) nsc[m] = 1.0f;
         if constexpr (NORM) {
-            // the reference summation order needs the whole row in one place
+            // the reference summation order needs each whole row in one place: f32 rows
+            // [M][K] in LDS, one wave per row
             float* lds_x = reinterpret_cast<float*>(smem);
 #pragma unroll
             for (int i = 0; i < XR; ++i) {
-                const int g = tid + NT * i;
-                if (i < gpt && g < ngroups) {
+                const int m = MR == 1 ? 0 : i / gpt, g = tid + NT * (i - m * gpt);
+                if (i < nreg && g < ngroups) {
                     float v[8];
                     xr[i].get(v);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) lds_x[8 * g + e] = v[e];
+                    for (int e = 0; e < 8; ++e) lds_x[m * p.K + 8 * g + e] = v[e];
                 }
             }
             lds_barrier();
-            if (tid < 64) {
-                const float sum = (p.flags & kFlagNormSeq) != 0 ? (tid == 0 ? lds_sumsq_seq(lds_x, p.K) : 0.0f)  // src/ops/norm.rs:38
-                                                                : lds_sumsq_neon16(lds_x, p.K);  // src/model/cpu.rs:14-35
-                if (tid == 0) s_inv[0] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+            if (wave < p.M) {
+                const float* xm = lds_x + wave * p.K;
+                const float sum = (p.flags & kFlagNormSeq) != 0 ? (lane == 0 ? lds_sumsq_seq(xm, p.K) : 0.0f)  // src/ops/norm.rs:38
+                                                                : lds_sumsq_neon16(xm, p.K);  // src/model/cpu.rs:14-35
+                if (lane == 0) s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
             }
             lds_barrier();
-            nscale = s_inv[0];
-            lds_barrier();  // lds_x is overwritten by the quantized row below
+#pragma unroll
+            for (int m = 0; m < MR; ++m) nsc[m] = m < p.M ? s_inv[m] : 1.0f;
+            lds_barrier();  // lds_x is overwritten by the quantized rows below
         }
         const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
         if (owner_wave) {
@@ -724,8 +753,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
 #pragma unroll
                             for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
                             if constexpr (NORM) {
+                                float ns = 1.0f;
 #pragma unroll
-                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int mm = 0; mm < MR; ++mm)
+                                    if (mm == m) ns = nsc[mm];
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
                             }
                             lm = 0.0f;
 #pragma unroll
@@ -775,9 +808,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             if (!bad_rows) {
                 // finite rows (the usual case): the short rounding sequence
                 if (rne)
-                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
                 else
-                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nscale, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
             } else {
 #pragma unroll
                 for (int i = 0; i < XR; ++i) {
@@ -787,8 +820,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                             float v[8];
                             xr[i].get(v);
                             if constexpr (NORM) {
+                                float ns = 1.0f;
 #pragma unroll
-                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * nscale) * gr[i][e];
+                                for (int mm = 0; mm < MR; ++mm)
+                                    if (mm == m) ns = nsc[mm];
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
                             }
                             float im = 1.0f;
 #pragma unroll
@@ -900,7 +937,9 @@ bool gemv_can_fuse(int M, int K, int waves, bool norm) {
     const int nt = 64 * waves;
     const int gpt = (K / 8 + nt - 1) / nt;
     if (K % 8 || M > kFusedMaxRows || M * gpt > fused_regs(waves)) return false;
-    if (norm && (M != 1 || (size_t)K * 4 > 64 * 1024)) return false;
+    if (norm && (size_t)M * K * 4 > 64 * 1024) return false;  // f32 rows of the RMSNorm in LDS
+    // (1024-thread workgroups would spill the per-slot gamma registers)
+    if (norm && M > 1 && (waves > 8 || M * gpt > kNormRowsRegs)) return false;
     return true;
 }
 
@@ -937,7 +976,9 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
 
 template <int BITS, bool SWIGLU, int MODE>
 static hipError_t launch_m(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
-    if (p.gamma) return launch_w<BITS, SWIGLU, MODE, true, 1>(p, waves, lds, st);  // fused norm: one row
+    if (p.gamma)  // fused RMSNorm
+        return p.M == 1 ? launch_w<BITS, SWIGLU, MODE, true, 1>(p, waves, lds, st)
+                        : launch_w<BITS, SWIGLU, MODE, true, 4>(p, waves, lds, st);
     if (p.M == 1) return launch_w<BITS, SWIGLU, MODE, false, 1>(p, waves, lds, st);
     return launch_w<BITS, SWIGLU, MODE, false, 4>(p, waves, lds, st);
 }

@@ -97,3 +97,36 @@ def test_item_width_matches_oracle(oracle, ws, iw, bits, N, swiglu):
         assert np.array_equal(f16_bits(out), f16_bits(ref))
         check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, swiglu), swiglu, torch.float16)
     w.close()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("order", ["neon16", "seq"])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_rmsnorm_rows_fused(oracle, ws, bits, order, M):
+    """RMSNorm of 2-4 rows inside the GEMV prologue (one wave per row sums its squares):
+    against the oracle, and bit for bit against the separate RMSNorm-quantize launch
+    (QLIN_NO_FUSED_QUANT) and the one-item-per-workgroup launch, fp16 and f32 rows."""
+    K = 2560
+    flags0 = ql.QLIN_NORM_SEQUENTIAL if order == "seq" else 0
+    for N, swiglu in ((2 * 16 * 600, True), (16 * 300, False), (2560, False)):
+        codes = synth.codes(N, K, bits, 320 + bits + N % 7).numpy()
+        sc = synth.scales(N, bits, 321 + bits).numpy()
+        w = make_weights(bits, codes, sc)
+        A = synth.activations(M, K, seed=322 + M, dist="student_t3")
+        gam = synth.gamma(K, seed=323)
+        flags = flags0 | (ql.QLIN_SWIGLU if swiglu else 0)
+        x = oracle.rmsnorm(A.float().numpy(), gam.numpy(), 1e-6, order)
+        q, s, _ = oracle.quantize(x, 0)
+        expect = oracle.dequant(oracle.gemm_i32_nk(q, codes), s, sc)
+        if swiglu:
+            expect = oracle.swiglu(expect)
+        for dt in (torch.float16, torch.float32):
+            a = A.to(DEV).to(dt)
+            out, ref = run_both(ws, w, a, out_dtype=torch.float16, flags=flags, gamma=gam.to(DEV), eps=1e-6)
+            sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags | ql.QLIN_NO_FUSED_QUANT,
+                         gamma=gam.to(DEV), eps=1e-6)
+            torch.cuda.synchronize()
+            assert np.array_equal(f16_bits(out), f16_bits(ref)), (N, dt)
+            assert np.array_equal(f16_bits(out), f16_bits(sep)), (N, dt)
+            check_outputs(oracle, out, expect, swiglu, torch.float16)
+        w.close()

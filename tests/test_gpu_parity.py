@@ -231,7 +231,7 @@ def test_qwen3_layer(oracle, ws, M):
         w.close()
 
 
-@pytest.mark.parametrize("M", [1, 3, 600])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 600])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_rmsnorm_linear(oracle, ws, M, bits):
     K, N = 2560, 2048
