@@ -502,6 +502,8 @@ int gemv_width(const qlin_weights* w, bool sw, int cus) {
     return gemv_item_width(sw ? w->N / 2 : w->N, cus);
 }
 
+int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm);
+
 int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
              const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
              int64_t ldc, uint32_t flags, hipStream_t st, const ResidualArgs* res = nullptr) {
@@ -542,7 +544,7 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
         waves = tuned_variant(w->bits, w->K, w->N, rows, A ? 0 : 1, sw);
         // a tuned count must still let the fused prologue hold the rows in registers
         if ((waves != 4 && waves != 8 && waves != 16) || (A && !gemv_can_fuse(rows, w->K, waves, gamma != nullptr)))
-            waves = gemv_pick_waves(groups, steps);
+            waves = A ? gemv_fused_waves(rows, w->K, groups, steps, gamma != nullptr) : gemv_pick_waves(groups, steps);
     }
     // More items than CUs with the quantization fused: one workgroup per CU (at most
     // four items each), so each CU quantizes the rows once.
@@ -555,6 +557,20 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     return launch_gemv(p, w->bits, waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
+// Waves per workgroup for a GEMV that quantizes (and normalizes) its rows itself: the
+// usual count, or for up to 3 rows fewer when that many threads cannot hold the rows in
+// registers (3 rows of K = 4096 at 16 waves); 0 when no count can.  Measured on o / down
+// shapes (N = 2560, µs per launch, fused at fewer waves vs separate quantize launch): W8
+// K = 4096 3 rows 6.94 vs 7.38, 4 rows 7.79 vs 7.50 (every workgroup re-reads and
+// quantizes all rows, so 4 rows keep the separate launch); K = 9728 2 rows 10.99 vs 10.96.
+int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm) {
+    for (int w = gemv_pick_waves(groups, steps); w >= 4; w /= 2) {
+        if (gemv_can_fuse(rows, K, w, norm)) return w;
+        if (rows >= 4) break;
+    }
+    return 0;
+}
+
 // Whether the decode GEMV may quantize (and normalize) the raw rows itself.
 bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, const float* gamma, uint32_t flags) {
     if (rows > kGemvMaxRows || (flags & kFlagNoFusedQuant) || rows > env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4))
@@ -565,8 +581,8 @@ bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, c
     const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
     const int cols = sw ? w->N / 2 : w->N;
     const int iw = gemv_width(w, sw, cu_count(w->device));
-    const int waves = gemv_pick_waves((cols + iw - 1) / iw, steps);
-    return gemv_can_fuse(rows, w->K, waves, gamma != nullptr) &&
+    const int waves = gemv_fused_waves(rows, w->K, (cols + iw - 1) / iw, steps, gamma != nullptr);
+    return waves != 0 &&
            (env_int("QLIN_GEMV_WAVES", 0) == 0 || gemv_can_fuse(rows, w->K, env_int("QLIN_GEMV_WAVES", 0), gamma != nullptr));
 }
 

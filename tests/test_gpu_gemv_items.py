@@ -130,3 +130,29 @@ def test_rmsnorm_rows_fused(oracle, ws, bits, order, M):
             assert np.array_equal(f16_bits(out), f16_bits(sep)), (N, dt)
             check_outputs(oracle, out, expect, swiglu, torch.float16)
         w.close()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K", [4096, 9728])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_fused_rows_fewer_waves(oracle, bits, K, M):
+    """o / down shapes (N = 2560): where 16-wave workgroups cannot hold up to 3 rows in
+    registers the GEMV takes fewer waves and still quantizes itself (K = 4096 3 rows,
+    K = 9728 2 rows; 4 rows there quantize in a separate launch); every case equals the
+    separate-quantize launch bit for bit and the oracle."""
+    N = 2560
+    ws = ql.Workspace(4, K, N)  # the separate quantization needs room for K columns
+    codes = synth.codes(N, K, bits, 330 + bits + K % 11).numpy()
+    sc = synth.scales(N, bits, 331 + bits).numpy()
+    w = make_weights(bits, codes, sc)
+    A = synth.activations(M, K, seed=332 + M)
+    expect = oracle_linear(oracle, A, codes, sc, False)
+    for dt in (torch.float16, torch.float32):
+        a = A.to(DEV).to(dt)
+        out = ql.run(ws, w, a, out_dtype=torch.float16)
+        sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=ql.QLIN_NO_FUSED_QUANT)
+        torch.cuda.synchronize()
+        assert np.array_equal(f16_bits(out), f16_bits(sep)), dt
+        check_outputs(oracle, out, expect, False, torch.float16)
+    w.close()
+    ws.close()
