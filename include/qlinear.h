@@ -19,7 +19,14 @@
  * frees them with the paired *_free.  Host buffers passed to *_create are copied.
  * Entry points taking `stream` are asynchronous and stream-ordered (stream is a
  * hipStream_t, NULL = default stream); pointers passed to them are device
- * pointers.  One workspace must not be used by two streams at once.
+ * pointers.
+ *
+ * A workspace holds shared scratch (quantized rows, per-token scales, the sticky error
+ * word, split-K partial sums and self-resetting split-K counters): it serves one stream
+ * at a time.  Two streams running on one workspace at once race on all of it, and a
+ * split-K counter left mid-count corrupts later GEMMs; give each stream its own
+ * workspace.  The output C of a run must not overlap its input A (the decode GEMV reads
+ * A while other workgroups already store C); qlin_run_residual may update R in place.
  */
 #ifndef QLINEAR_H
 #define QLINEAR_H
@@ -156,9 +163,9 @@ int qlin_run_f32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, 
                  float* C);
 
 /* Replaces rk_npu_w4a8_run_swiglu_f32 (src/npu.rs:1044-1046): C is [rows, N/2].
- * Needs N % 64 == 0 (the reference's own condition, src/npu.rs:1011); otherwise
- * returns QLIN_ERR_UNSUPPORTED and the caller runs qlin_run_f32 + its own SwiGLU,
- * as the reference caller does when run_swiglu returns false. */
+ * Any even N (the reference fuses only for N % 64 == 0, src/npu.rs:1011, and otherwise
+ * falls back to its CPU SwiGLU; here every even N is fused).  Odd N returns
+ * QLIN_ERR_UNSUPPORTED. */
 int qlin_run_swiglu_f32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
                         const float* A, float* C);
 
@@ -211,6 +218,37 @@ int qlin_gemm_i32(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
 int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* weights, int32_t rows,
                        const int8_t* q, int64_t ldq, const float* s, void* C, int32_t c_dtype,
                        int64_t ldc, uint32_t flags, void* stream);
+
+/* SiLU-gate on the unfused layout, on the device: Y[m, j] = SiLU(X[m, j]) * X[m, F + j],
+ * j < F, rows of X holding the gate block then the up block ([rows, 2F], stride ldx >= 2F)
+ * and Y [rows, F] (stride ldy >= F), f32 or fp16 each.  Replaces the reference's CPU
+ * fallback Cpu::swiglu / swiglu_block (src/model/cpu.rs:119-152,327-351), used when the
+ * fused SwiGLU declines (src/model/dense.rs:508-522).  Same SiLU as the fused epilogue. */
+int qlin_swiglu(int32_t rows, int32_t F, const void* X, int32_t x_dtype, int64_t ldx, void* Y, int32_t y_dtype,
+                int64_t ldy, void* stream);
+
+/* ---- launch plan (debug tap) ----
+ * Describes the launches qlin_run (gamma NULL) or qlin_run_rmsnorm would make for these
+ * arguments, without launching anything: A and gamma are only inspected for alignment.
+ * No counterpart in the reference, whose library reports its strategy through
+ * rk_npu_w4a8_query / backend stats (src/npu.rs:631-661). */
+#define QLIN_PATH_GEMV_FUSED 0 /* one GEMV launch that quantizes (and normalizes) its rows itself */
+#define QLIN_PATH_GEMV 1       /* a quantize launch, then the GEMV on the quantized rows */
+#define QLIN_PATH_GEMM 2       /* a quantize launch, then the MFMA GEMM */
+typedef struct qlin_plan {
+    int32_t path;       /* QLIN_PATH_* */
+    int32_t launches;   /* kernel launches of the call */
+    int32_t waves;      /* waves per workgroup of the GEMV / GEMM */
+    int32_t item_width; /* GEMV: output channels per item */
+    int32_t items;      /* GEMV items, or GEMM output tiles */
+    int32_t grid;       /* workgroups of the GEMV / GEMM launch */
+    int32_t splits;     /* GEMM: k splits per tile */
+    int32_t tile_m;     /* GEMM: rows per tile */
+    int32_t tile_n;     /* GEMM: output channels per tile */
+    int32_t reserved[3];
+} qlin_plan;
+int qlin_run_plan(const qlin_workspace* ws, const qlin_weights* weights, int32_t rows, const void* A, int64_t lda,
+                  const float* gamma, uint32_t flags, qlin_plan* out);
 
 /* ---- kernel-variant selection ----
  * Replaces the NPU strategy search and its on-disk cache (src/npu.rs:595-996, driven by
@@ -266,6 +304,12 @@ void qlin_chain_free(qlin_chain* chain);
 int qlin_chain_run(qlin_chain* chain, int32_t rows, const void* x, int64_t ldx, void* y, int64_t ldy,
                    void* stream);
 
+/* Polls of a stage counter (each followed by a short sleep) before a workgroup gives up
+ * waiting and sets the QLIN_ERR_DEVICE bit of the chain's error word.  Default 4194304
+ * (~0.2 s; QLIN_CHAIN_SPIN_LIMIT at chain creation overrides it); 0 gives up at once,
+ * which tests use to exercise the failure path without any kernel hanging. */
+int qlin_chain_set_wait_limit(qlin_chain* chain, int32_t polls);
+
 /* Device pointer and row stride (elements) of stage `stage`'s fp16 output from the
  * last run (the last stage writes y instead). */
 int qlin_chain_stage_output(const qlin_chain* chain, int32_t stage, void** ptr, int64_t* ld);
@@ -273,7 +317,9 @@ int qlin_chain_stage_output(const qlin_chain* chain, int32_t stage, void** ptr, 
 /* Error word of the runs since the last clear: QLIN_OK, QLIN_ERR_NONFINITE (an input
  * row held Inf/NaN) or QLIN_ERR_DEVICE (a stage wait gave up: the grid was not fully
  * resident, e.g. other work occupied the GPU; the outputs are then invalid).
- * Synchronizes the last run's stream.  clear != 0 resets the word. */
+ * Synchronizes the last run's stream.  clear != 0 resets the word.  After a run that
+ * gave up, the stage counters may be left mid-count: call qlin_chain_status (which
+ * restarts them from zero) before the chain runs again. */
 int qlin_chain_status(qlin_chain* chain, int32_t clear);
 
 #ifdef __cplusplus

@@ -30,6 +30,10 @@ QLIN_SWIGLU = 0x4
 QLIN_NO_FUSED_QUANT = 0x8
 QLIN_RESIDUAL = 0x10
 
+QLIN_PATH_GEMV_FUSED = 0
+QLIN_PATH_GEMV = 1
+QLIN_PATH_GEMM = 2
+
 QLIN_PACK_QUANTIZED = 0
 QLIN_INT_QUANTIZED = 1
 
@@ -71,6 +75,9 @@ SIGNATURES = {
     "qlin_chain_run": (ctypes.c_int, [_P, _I32, _P, _I64, _P, _I64, _P]),
     "qlin_chain_stage_output": (ctypes.c_int, [_P, _I32, _P, _P]),
     "qlin_chain_status": (ctypes.c_int, [_P, _I32]),
+    "qlin_chain_set_wait_limit": (ctypes.c_int, [_P, _I32]),
+    "qlin_swiglu": (ctypes.c_int, [_I32, _I32, _P, _I32, _I64, _P, _I32, _I64, _P]),
+    "qlin_run_plan": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _U32, _P]),
 }
 
 
@@ -91,6 +98,11 @@ class WorkspaceInfo(ctypes.Structure):
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("device", _I32), ("cu_count", _I32), ("arch", _I32), ("reserved", _I32),
                 ("sclk_khz", _I64), ("mclk_khz", _I64), ("bus_width_bits", _I64), ("hbm_bytes", _I64)]
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("path", _I32), ("launches", _I32), ("waves", _I32), ("item_width", _I32), ("items", _I32),
+                ("grid", _I32), ("splits", _I32), ("tile_m", _I32), ("tile_n", _I32), ("reserved", _I32 * 3)]
 
 
 class ChainStage(ctypes.Structure):

@@ -1,11 +1,13 @@
-"""Builds libqlinear.so (the HIP kernels, the C ABI and the C++ npu mirror) in-tree
-for gfx950, the native test binary tests/cpp/_build/npu_backend_test and the hardware
-calibration probes probes/_build/hw_probes.
+"""Builds libqlinear.so and libqlinear.a (the HIP kernels, the C ABI and the C++ npu
+mirror) in-tree for gfx950, and the native test binaries under tests/cpp/_build: the
+npu mirror's test and a C program linked against the static archive.
 
     python -m open_rknpu2_lm_infer_amd.build
 
 Every .hip / .cpp file under csrc/ is compiled to an object in parallel with hipcc,
-then linked into open_rknpu2_lm_infer_amd/libqlinear.so next to this file.  Device code
+then linked into open_rknpu2_lm_infer_amd/libqlinear.so next to this file and archived
+into libqlinear.a (the form a Rust build.rs links: the archive whole, plus -lamdhip64
+and the C++ runtime).  Device code
 is compiled with single-rounding IEEE semantics: no FP contraction, correctly
 rounded f32 divide and sqrt, denormals kept, packed-FP32 instructions disabled.
 """
@@ -19,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqlinear.so")
+STATIC_LIB = os.path.join(HERE, "libqlinear.a")
 ARCH = os.environ.get("QLIN_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -46,8 +49,8 @@ ROOT = os.path.dirname(HERE)
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "npu_backend_test.cpp")
 TEST_BUILD = os.path.join(ROOT, "tests", "cpp", "_build")
 TEST_BIN = os.path.join(TEST_BUILD, "npu_backend_test")
-PROBE_SRC = os.path.join(HERE, "probes", "hw_probes.hip")
-PROBE_BIN = os.path.join(HERE, "probes", "_build", "hw_probes")
+STATIC_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "static_link_test.c")
+STATIC_TEST_BIN = os.path.join(TEST_BUILD, "static_link_test")
 
 
 def sources():
@@ -80,8 +83,12 @@ def build(verbose: bool = False) -> str:
            "-Wl,-rpath,/opt/rocm/lib"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    tmp = STATIC_LIB + ".tmp"
+    if os.path.exists(tmp):
+        os.remove(tmp)
+    subprocess.run(["ar", "rcs", tmp, *objs], check=True)
+    os.replace(tmp, STATIC_LIB)
     build_tests()
-    build_probes()
     return LIB
 
 
@@ -93,16 +100,12 @@ def build_tests() -> str:
                     os.path.join(ROOT, "oracle", "qlin_oracle.c"), "-o", oracle_obj], check=True)
     subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", TEST_SRC, oracle_obj, "-o", TEST_BIN,
                     f"-L{HERE}", "-lqlinear", "-Wl,-rpath,$ORIGIN/../../../open_rknpu2_lm_infer_amd", "-lm"], check=True)
+    # a C caller of the static archive, linked as a Rust build.rs would link it
+    static_obj = os.path.join(TEST_BUILD, "static_link_test.o")
+    subprocess.run(["gcc", "-O2", "-std=c11", "-Wall", "-c", STATIC_TEST_SRC, "-o", static_obj], check=True)
+    subprocess.run(["g++", static_obj, "-o", STATIC_TEST_BIN, "-Wl,--whole-archive", STATIC_LIB,
+                    "-Wl,--no-whole-archive", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"], check=True)
     return TEST_BIN
-
-
-def build_probes() -> str:
-    """Calibration probes (MFMA rate, LDS copy rate, LDS read patterns, launch floors);
-    the MFMA chains stay in VGPRs as in the GEMM."""
-    os.makedirs(os.path.dirname(PROBE_BIN), exist_ok=True)
-    subprocess.run([HIPCC, *[f for f in COMMON if f not in ("-fPIC",)], "-mllvm", "-amdgpu-mfma-vgpr-form",
-                    PROBE_SRC, "-o", PROBE_BIN], check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-    return PROBE_BIN
 
 
 if __name__ == "__main__":

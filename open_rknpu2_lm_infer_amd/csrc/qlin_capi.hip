@@ -28,8 +28,23 @@ struct qlin_weights {
     float* scales;
 };
 
+// Environment overrides of the kernel-variant choices (tests, tuning experiments), read
+// once when a workspace is created so the run path makes no getenv calls.  0 / -1: unset.
+struct QlinOverrides {
+    int gemv_item_width;  // QLIN_GEMV_ITEM_WIDTH, 1..16
+    int gemv_waves;       // QLIN_GEMV_WAVES, 4 / 8 / 16
+    int gemv_grid;        // QLIN_GEMV_GRID, >= 0 (0: one workgroup per item)
+    int fused_max_rows;   // QLIN_FUSED_QUANT_MAX_ROWS (default 4)
+    int gemm_splits;      // QLIN_GEMM_SPLITS
+    int gemm_target_wgs;  // QLIN_GEMM_TARGET_WGS (default: the CU count)
+    int gemm_group_m;     // QLIN_GEMM_GROUP_M (default 4)
+    int gemm_deep;        // QLIN_GEMM_DEEP, 0 / 1
+    int gemm_wn;          // QLIN_GEMM_WN, 2 / 4
+};
+
 struct qlin_workspace {
     int max_rows, max_k, max_n, max_kp, max_np, device, cu_count;
+    QlinOverrides ov;
     int8_t* q;           // [max_rows, max_kp]
     float* s;            // [max_rows]
     uint32_t* counters;  // [n_counters], zero at rest
@@ -55,6 +70,20 @@ int env_int(const char* name, int dflt) {
     return v && *v ? std::atoi(v) : dflt;
 }
 
+QlinOverrides read_overrides() {
+    QlinOverrides o;
+    o.gemv_item_width = env_int("QLIN_GEMV_ITEM_WIDTH", 0);
+    o.gemv_waves = env_int("QLIN_GEMV_WAVES", 0);
+    o.gemv_grid = env_int("QLIN_GEMV_GRID", -1);
+    o.fused_max_rows = env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4);
+    o.gemm_splits = env_int("QLIN_GEMM_SPLITS", 0);
+    o.gemm_target_wgs = env_int("QLIN_GEMM_TARGET_WGS", 0);
+    o.gemm_group_m = env_int("QLIN_GEMM_GROUP_M", 4);
+    o.gemm_deep = env_int("QLIN_GEMM_DEEP", -1);
+    o.gemm_wn = env_int("QLIN_GEMM_WN", 4);
+    return o;
+}
+
 int current_device(int* dev) { return hipGetDevice(dev) == hipSuccess ? QLIN_OK : QLIN_ERR_NODEVICE; }
 
 // ---- kernel-variant table (qlin_tune) ------------------------------------------------
@@ -70,6 +99,7 @@ std::mutex& tune_mutex() {
     return m;
 }
 thread_local int g_force_variant = 0;  // set by qlin_tune while it times one candidate
+std::atomic<int> g_tune_entries{0};    // entries in the table: the run path skips the lock at 0
 
 int rows_bucket(int rows) {
     if (rows <= kGemvMaxRows) return rows;
@@ -80,6 +110,7 @@ int rows_bucket(int rows) {
 
 int tuned_variant(int bits, int K, int N, int rows, int path, bool sw) {
     if (g_force_variant) return g_force_variant;
+    if (g_tune_entries.load(std::memory_order_acquire) == 0) return 0;
     std::lock_guard<std::mutex> g(tune_mutex());
     auto it = tune_table().find(TuneKey{bits, K, N, rows_bucket(rows), path, sw ? 1 : 0});
     return it == tune_table().end() ? 0 : it->second;
@@ -404,6 +435,7 @@ int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_w
     ws->max_np = (int)round_up(max_n, kNAlign);
     ws->device = dev;
     ws->cu_count = cu_count(dev);
+    ws->ov = read_overrides();
     ws->n_counters = std::max(ws->max_np / 16, 8192);
     const size_t bq = (size_t)max_rows * ws->max_kp, bs = (size_t)max_rows * sizeof(float);
     const size_t bc = (size_t)ws->n_counters * sizeof(uint32_t);
@@ -486,8 +518,6 @@ int qlin_quantize(int32_t rows, int32_t K, const void* A, int32_t a_dtype, int64
 
 namespace {
 
-// Output channels per GEMV item: QLIN_GEMV_ITEM_WIDTH (1..16) if set, else the width in
-// 8..16 that spreads the items most evenly over the CUs.
 // Residual update of the epilogue (qlin_run_residual, chain stages with QLIN_RESIDUAL).
 struct ResidualArgs {
     const void* R;
@@ -496,18 +526,70 @@ struct ResidualArgs {
     float mult;
 };
 
-int gemv_width(const qlin_weights* w, bool sw, int cus) {
-    const int forced = env_int("QLIN_GEMV_ITEM_WIDTH", 0);
-    if (forced >= 1 && forced <= 16) return forced;
-    return gemv_item_width(sw ? w->N / 2 : w->N, cus);
+// Waves per workgroup for a GEMV that quantizes (and normalizes) its rows itself: the
+// usual count, or for up to 3 rows fewer when that many threads cannot hold the rows in
+// registers (3 rows of K = 4096 at 16 waves); 0 when no count can.  Measured on o / down
+// shapes (N = 2560, us per launch, fused at fewer waves vs separate quantize launch): W8
+// K = 4096 3 rows 6.94 vs 7.38, 4 rows 7.79 vs 7.50 (every workgroup re-reads and
+// quantizes all rows, so 4 rows keep the separate launch); K = 9728 2 rows 10.99 vs 10.96.
+int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm) {
+    for (int w = gemv_pick_waves(groups, steps); w >= 4; w /= 2) {
+        if (gemv_can_fuse(rows, K, w, norm)) return w;
+        if (rows >= 4) break;
+    }
+    return 0;
 }
 
-int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm);
+// Launch shape of a decode GEMV.
+struct GemvPlan {
+    int iw;     // output channels per item (QLIN_GEMV_ITEM_WIDTH, else the width in 8..16
+                // that spreads the items most evenly over the CUs)
+    int waves;  // waves per workgroup: 4, 8 or 16; 0 = the fused prologue cannot hold the rows
+    int grid;   // workgroups; 0 = one per item
+    int items;  // items of the launch
+};
+
+GemvPlan plan_gemv(const qlin_workspace* ws, const qlin_weights* w, int rows, bool fused, bool norm, uint32_t flags) {
+    const QlinOverrides& ov = ws->ov;
+    const bool sw = (flags & kFlagSwiglu) != 0;
+    const int cols = sw ? w->N / 2 : w->N;
+    GemvPlan g{};
+    g.iw = ov.gemv_item_width >= 1 && ov.gemv_item_width <= 16 ? ov.gemv_item_width : gemv_item_width(cols, ws->cu_count);
+    g.items = (cols + g.iw - 1) / g.iw;
+    const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
+    int waves = ov.gemv_waves;
+    if (waves != 4 && waves != 8 && waves != 16) {
+        waves = tuned_variant(w->bits, w->K, w->N, rows, fused ? 0 : 1, sw);
+        // a tuned count must still let the fused prologue hold the rows in registers
+        if ((waves != 4 && waves != 8 && waves != 16) || (fused && !gemv_can_fuse(rows, w->K, waves, norm)))
+            waves = fused ? gemv_fused_waves(rows, w->K, g.items, steps, norm) : gemv_pick_waves(g.items, steps);
+    } else if (fused && !gemv_can_fuse(rows, w->K, waves, norm)) {
+        waves = 0;
+    }
+    g.waves = waves;
+    // More items than CUs with the quantization fused: one workgroup per CU (at most
+    // four items each), so each CU quantizes the rows once.
+    if (ov.gemv_grid >= 0)
+        g.grid = ov.gemv_grid;
+    else if (fused && g.items > ws->cu_count)
+        g.grid = std::max(ws->cu_count, (g.items + 3) / 4);
+    return g;
+}
+
+// Whether the decode GEMV may quantize (and normalize) the raw rows itself.
+bool gemv_fusable(const qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int64_t lda,
+                  const float* gamma, uint32_t flags) {
+    if (rows > kGemvMaxRows || (flags & kFlagNoFusedQuant) || rows > ws->ov.fused_max_rows) return false;
+    if ((reinterpret_cast<uintptr_t>(A) & 15) || (lda % 8) || (gamma && (reinterpret_cast<uintptr_t>(gamma) & 15)))
+        return false;
+    return plan_gemv(ws, w, rows, true, gamma != nullptr, flags).waves != 0;
+}
 
 int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A, int a_f16, int64_t lda,
              const float* gamma, float eps, const int8_t* q, int64_t ldq, const float* s, void* C, int c_kind,
              int64_t ldc, uint32_t flags, hipStream_t st, const ResidualArgs* res = nullptr) {
-    const bool sw = (flags & kFlagSwiglu) != 0;
+    const GemvPlan g = plan_gemv(ws, w, rows, A != nullptr, gamma != nullptr, flags);
+    if (g.waves == 0) return QLIN_ERR_UNSUPPORTED;  // callers check gemv_fusable first
     GemvParams p{};
     if (res) {
         p.R = res->R;
@@ -536,59 +618,56 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     p.c_kind = c_kind;
     p.flags = flags;
     p.err = ws->err;
-    const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
-    p.iw = gemv_width(w, sw, ws->cu_count);
-    const int groups = gemv_items(p);
-    int waves = env_int("QLIN_GEMV_WAVES", 0);
-    if (waves != 4 && waves != 8 && waves != 16) {
-        waves = tuned_variant(w->bits, w->K, w->N, rows, A ? 0 : 1, sw);
-        // a tuned count must still let the fused prologue hold the rows in registers
-        if ((waves != 4 && waves != 8 && waves != 16) || (A && !gemv_can_fuse(rows, w->K, waves, gamma != nullptr)))
-            waves = A ? gemv_fused_waves(rows, w->K, groups, steps, gamma != nullptr) : gemv_pick_waves(groups, steps);
-    }
-    // More items than CUs with the quantization fused: one workgroup per CU (at most
-    // four items each), so each CU quantizes the rows once.
-    const int cus = ws->cu_count;
-    const int grid_env = env_int("QLIN_GEMV_GRID", -1);
-    if (grid_env >= 0)
-        p.grid = grid_env;
-    else if (A && groups > cus)
-        p.grid = std::max(cus, (groups + 3) / 4);
-    return launch_gemv(p, w->bits, waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+    p.iw = g.iw;
+    p.grid = g.grid;
+    return launch_gemv(p, w->bits, g.waves, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
-// Waves per workgroup for a GEMV that quantizes (and normalizes) its rows itself: the
-// usual count, or for up to 3 rows fewer when that many threads cannot hold the rows in
-// registers (3 rows of K = 4096 at 16 waves); 0 when no count can.  Measured on o / down
-// shapes (N = 2560, µs per launch, fused at fewer waves vs separate quantize launch): W8
-// K = 4096 3 rows 6.94 vs 7.38, 4 rows 7.79 vs 7.50 (every workgroup re-reads and
-// quantizes all rows, so 4 rows keep the separate launch); K = 9728 2 rows 10.99 vs 10.96.
-int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm) {
-    for (int w = gemv_pick_waves(groups, steps); w >= 4; w /= 2) {
-        if (gemv_can_fuse(rows, K, w, norm)) return w;
-        if (rows >= 4) break;
-    }
-    return 0;
-}
+// Launch shape of a prefill GEMM.
+struct GemmPlan {
+    int bn, m_tiles, n_tiles, splits, ktiles_per_split, group_m, deep, wn;
+};
 
-// Whether the decode GEMV may quantize (and normalize) the raw rows itself.
-bool gemv_fusable(const qlin_weights* w, int rows, const void* A, int64_t lda, const float* gamma, uint32_t flags) {
-    if (rows > kGemvMaxRows || (flags & kFlagNoFusedQuant) || rows > env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4))
-        return false;
-    if ((reinterpret_cast<uintptr_t>(A) & 15) || (lda % 8) || (gamma && (reinterpret_cast<uintptr_t>(gamma) & 15)))
-        return false;
+int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags, GemmPlan* out) {
+    const QlinOverrides& ov = ws->ov;
     const bool sw = (flags & kFlagSwiglu) != 0;
-    const int steps = w->Kp / (w->bits == 4 ? 256 : 128);
-    const int cols = sw ? w->N / 2 : w->N;
-    const int iw = gemv_width(w, sw, cu_count(w->device));
-    const int waves = gemv_fused_waves(rows, w->K, (cols + iw - 1) / iw, steps, gamma != nullptr);
-    return waves != 0 &&
-           (env_int("QLIN_GEMV_WAVES", 0) == 0 || gemv_can_fuse(rows, w->K, env_int("QLIN_GEMV_WAVES", 0), gamma != nullptr));
+    GemmPlan g{};
+    g.bn = gemm_tile_n(w->bits, w->N);
+    const int cols = sw ? g.bn / 2 : g.bn;  // output channels per tile
+    g.m_tiles = (rows + kGemmTileM - 1) / kGemmTileM;
+    g.n_tiles = ((sw ? w->N / 2 : w->N) + cols - 1) / cols;
+    const int ktiles = w->Kp / kGemmTileK;
+    const int tiles = g.m_tiles * g.n_tiles;
+    const int64_t slice = (int64_t)gemm_regs_per_thread(g.bn) * 256;  // ints of one partial tile
+    int S = ov.gemm_splits;
+    if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
+    if (S <= 0) {
+        // split K until the grid covers the CUs, keeping >= 4 k tiles per split
+        // split-K's partial round trip costs more than a second resident workgroup
+        // per CU gains, so the target is one workgroup per CU
+        const int target = ov.gemm_target_wgs > 0 ? ov.gemm_target_wgs : ws->cu_count;
+        S = (target + tiles / 2) / tiles;
+        S = std::min(S, std::max(1, ktiles / 4));
+    }
+    S = std::max(1, std::min(S, ktiles));
+    while (S > 1 && ((int64_t)tiles * S * slice > kGemmPartInts || tiles > ws->n_counters)) --S;
+    // the GEMM's k loop takes two tiles per iteration: Kp is a multiple of 256, so
+    // ktiles is even, and an even split size keeps every split's count even
+    if (ktiles % 2) return QLIN_ERR_PARAM;
+    g.ktiles_per_split = ((ktiles + S - 1) / S + 1) & ~1;
+    g.splits = (ktiles + g.ktiles_per_split - 1) / g.ktiles_per_split;
+    g.group_m = std::max(1, std::min(g.m_tiles, ov.gemm_group_m));
+    // a grid with at most one workgroup per CU takes the deeper pipeline
+    g.deep = ov.gemm_deep >= 0 ? (ov.gemm_deep != 0) : (int64_t)tiles * g.splits <= ws->cu_count;
+    g.wn = ov.gemm_wn == 2 ? 2 : 4;  // 2 x 4 waves unless QLIN_GEMM_WN=2
+    *out = g;
+    return QLIN_OK;
 }
 
 int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* q, int64_t ldq, const float* s,
              void* C, int c_kind, int64_t ldc, uint32_t flags, hipStream_t st, const ResidualArgs* res = nullptr) {
-    const bool sw = (flags & kFlagSwiglu) != 0;
+    GemmPlan g;
+    if (int rc = plan_gemm(ws, w, rows, flags, &g)) return rc;
     GemmParams p{};
     if (res) {
         p.R = res->R;
@@ -611,45 +690,24 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     p.ldc = ldc;
     p.c_kind = c_kind;
     p.flags = flags;
-    const int bn = gemm_tile_n(w->bits, w->N);
-    const int cols = sw ? bn / 2 : bn;  // output channels per tile
-    p.m_tiles = (rows + kGemmTileM - 1) / kGemmTileM;
-    p.n_tiles = ((sw ? w->N / 2 : w->N) + cols - 1) / cols;
-    const int ktiles = w->Kp / kGemmTileK;
-    const int tiles = p.m_tiles * p.n_tiles;
-    const int64_t slice = (int64_t)gemm_regs_per_thread(bn) * 256;  // ints of one partial tile
-    int S = env_int("QLIN_GEMM_SPLITS", 0);
-    if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
-    if (S <= 0) {
-        // split K until the grid covers the CUs, keeping >= 4 k tiles per split
-        // split-K's partial round trip costs more than a second resident workgroup
-        // per CU gains, so the target is one workgroup per CU
-        const int target = env_int("QLIN_GEMM_TARGET_WGS", ws->cu_count);
-        S = (target + tiles / 2) / tiles;
-        S = std::min(S, std::max(1, ktiles / 4));
-    }
-    S = std::max(1, std::min(S, ktiles));
-    while (S > 1 && ((int64_t)tiles * S * slice > kGemmPartInts || tiles > ws->n_counters)) --S;
-    // the GEMM's k loop takes two tiles per iteration: Kp is a multiple of 256, so
-    // ktiles is even, and an even split size keeps every split's count even
-    if (ktiles % 2) return QLIN_ERR_PARAM;
-    p.ktiles_per_split = ((ktiles + S - 1) / S + 1) & ~1;
-    p.splits = (ktiles + p.ktiles_per_split - 1) / p.ktiles_per_split;
-    p.group_m = std::max(1, std::min(p.m_tiles, env_int("QLIN_GEMM_GROUP_M", 4)));
+    p.m_tiles = g.m_tiles;
+    p.n_tiles = g.n_tiles;
+    p.ktiles_per_split = g.ktiles_per_split;
+    p.splits = g.splits;
+    p.group_m = g.group_m;
     p.part = ws->gemm_part;
     p.counters = ws->counters;
-    // a grid with at most one workgroup per CU takes the deeper pipeline
-    const int deep_env = env_int("QLIN_GEMM_DEEP", -1);
-    p.deep = deep_env >= 0 ? (deep_env != 0) : (int64_t)tiles * p.splits <= ws->cu_count;
-    p.wn = env_int("QLIN_GEMM_WN", 4) == 2 ? 2 : 4;  // 2 x 4 waves unless QLIN_GEMM_WN=2
-    return launch_gemm(p, w->bits, bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+    p.deep = g.deep;
+    p.wn = g.wn;
+    return launch_gemm(p, w->bits, g.bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
 int check_run(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags) {
     if (!ws || !w || rows <= 0 || rows > ws->max_rows) return QLIN_ERR_PARAM;
     if (w->Kp > ws->max_kp || w->Np > ws->max_np) return QLIN_ERR_PARAM;
     if (w->device != ws->device) return QLIN_ERR_PARAM;
-    if ((flags & kFlagSwiglu) && (w->N % 64 != 0)) return QLIN_ERR_UNSUPPORTED;
+    // SiLU-gate pairs column j with j + N/2: any even N
+    if ((flags & kFlagSwiglu) && (w->N & 1)) return QLIN_ERR_UNSUPPORTED;
     return QLIN_OK;
 }
 
@@ -664,7 +722,7 @@ int run_impl(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
     if (ldc < ncols) return QLIN_ERR_PARAM;
     if (gamma && !(eps > 0.0f && std::isfinite(eps))) return QLIN_ERR_PARAM;
     ws->last = st;
-    if (gemv_fusable(w, rows, A, lda, gamma, flags)) {
+    if (gemv_fusable(ws, w, rows, A, lda, gamma, flags)) {
         return run_gemv(ws, w, rows, A, a_dtype == QLIN_F16, lda, gamma, eps, nullptr, 0, nullptr, C,
                         c_dtype == QLIN_F16, ldc, flags, st, res);
     }
@@ -770,6 +828,54 @@ int qlin_run_quantized(qlin_workspace* ws, const qlin_weights* w, int32_t rows, 
     return run_gemm(ws, w, rows, q, ldq, s, C, c_dtype == QLIN_F16 ? 1 : 0, ldc, flags, st);
 }
 
+int qlin_run_plan(const qlin_workspace* ws, const qlin_weights* w, int32_t rows, const void* A, int64_t lda,
+                  const float* gamma, uint32_t flags, qlin_plan* out) {
+    if (!out || !A) return QLIN_ERR_PARAM;
+    if (int rc = check_run(ws, w, rows, flags)) return rc;
+    std::memset(out, 0, sizeof(*out));
+    if (gemv_fusable(ws, w, rows, A, lda, gamma, flags)) {
+        const GemvPlan g = plan_gemv(ws, w, rows, true, gamma != nullptr, flags);
+        out->path = QLIN_PATH_GEMV_FUSED;
+        out->launches = 1;
+        out->waves = g.waves;
+        out->item_width = g.iw;
+        out->items = g.items;
+        out->grid = g.grid > 0 && g.grid < g.items ? g.grid : g.items;
+        return QLIN_OK;
+    }
+    out->launches = 2;
+    if (gemv_ok(ws, w, rows)) {
+        const GemvPlan g = plan_gemv(ws, w, rows, false, false, flags);
+        out->path = QLIN_PATH_GEMV;
+        out->waves = g.waves;
+        out->item_width = g.iw;
+        out->items = g.items;
+        out->grid = g.items;
+        return QLIN_OK;
+    }
+    GemmPlan g;
+    if (int rc = plan_gemm(ws, w, rows, flags, &g)) return rc;
+    out->path = QLIN_PATH_GEMM;
+    out->waves = 2 * g.wn;
+    out->tile_m = kGemmTileM;
+    out->tile_n = (flags & kFlagSwiglu) ? g.bn / 2 : g.bn;
+    out->items = g.m_tiles * g.n_tiles;
+    out->splits = g.splits;
+    out->grid = out->items * g.splits;
+    return QLIN_OK;
+}
+
+int qlin_swiglu(int32_t rows, int32_t F, const void* X, int32_t x_dtype, int64_t ldx, void* Y, int32_t y_dtype,
+                int64_t ldy, void* stream) {
+    if (rows <= 0 || F <= 0 || !X || !Y || ldx < 2 * (int64_t)F || ldy < F ||
+        (x_dtype != QLIN_F32 && x_dtype != QLIN_F16) || (y_dtype != QLIN_F32 && y_dtype != QLIN_F16))
+        return QLIN_ERR_PARAM;
+    return launch_swiglu(rows, F, X, x_dtype == QLIN_F16, ldx, Y, y_dtype == QLIN_F16, ldy, (hipStream_t)stream) ==
+                   hipSuccess
+               ? QLIN_OK
+               : QLIN_ERR_DEVICE;
+}
+
 }  // extern "C"
 
 // ---- decode chain --------------------------------------------------------------
@@ -789,6 +895,7 @@ struct qlin_chain {
     std::vector<int64_t> ld;
     uint32_t* counters;
     uint32_t* err;
+    int spin_limit;  // polls per stage wait before the kernel gives up (QLIN_CHAIN_SPIN_LIMIT)
     hipStream_t last;
 };
 
@@ -813,6 +920,7 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
     c->n = n;
     c->max_rows = max_rows;
     c->device = dev;
+    c->spin_limit = env_int("QLIN_CHAIN_SPIN_LIMIT", 1 << 22);  // ~0.2 s of polling per wait
     c->stages.resize(n);
     c->cols.resize(n);
     c->outs.assign(n, nullptr);
@@ -929,13 +1037,19 @@ int qlin_chain_run(qlin_chain* c, int32_t rows, const void* x, int64_t ldx, void
     p.ldy = ldy;
     p.counters = c->counters;
     p.err = c->err;
-    p.spin_limit = env_int("QLIN_CHAIN_SPIN_LIMIT", 1 << 22);  // ~0.2 s of polling per wait
+    p.spin_limit = c->spin_limit;
     p.kp_max = c->kp_max;
     p.lds_q_bytes = (int)c->q_bytes;
     p.lds_red_bytes = (int)c->red_bytes;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     c->last = st;
     return launch_chain(p, c->grid, c->lds, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+}
+
+int qlin_chain_set_wait_limit(qlin_chain* c, int32_t polls) {
+    if (!c || polls < 0) return QLIN_ERR_PARAM;
+    c->spin_limit = polls;
+    return QLIN_OK;
 }
 
 int qlin_chain_stage_output(const qlin_chain* c, int32_t stage, void** ptr, int64_t* ld) {
@@ -974,7 +1088,7 @@ int qlin_tune(qlin_workspace* ws, const qlin_weights* w, int32_t rows, uint32_t 
         return QLIN_ERR_NOMEM;
     }
     int rc = hipMemset(A, 0x3c, a_bytes) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;  // every value 1.0 (0x3c3c)
-    const bool fused = gemv_fusable(w, rows, A, w->K, nullptr, flags);
+    const bool fused = gemv_fusable(ws, w, rows, A, w->K, nullptr, flags);
     const int path = fused ? 0 : (gemv_ok(ws, w, rows) ? 1 : 2);
     std::vector<int> cand;
     if (path < 2) {
@@ -1016,6 +1130,7 @@ int qlin_tune(qlin_workspace* ws, const qlin_weights* w, int32_t rows, uint32_t 
     if (!rc && best) {
         std::lock_guard<std::mutex> g(tune_mutex());
         tune_table()[TuneKey{w->bits, w->K, w->N, rows_bucket(rows), path, sw ? 1 : 0}] = best;
+        g_tune_entries.store((int)tune_table().size(), std::memory_order_release);
     }
     return rc;
 }
@@ -1028,6 +1143,7 @@ int qlin_tune_count(void) {
 void qlin_tune_clear(void) {
     std::lock_guard<std::mutex> g(tune_mutex());
     tune_table().clear();
+    g_tune_entries.store(0, std::memory_order_release);
 }
 
 int qlin_tune_save(const char* path) {
@@ -1061,6 +1177,7 @@ int qlin_tune_load(const char* path) {
         tune_table()[TuneKey{b, K, N, r, path_, swg}] = v;
         ++n;
     }
+    g_tune_entries.store((int)tune_table().size(), std::memory_order_release);
     std::fclose(f);
     return rc ? rc : n;
 }

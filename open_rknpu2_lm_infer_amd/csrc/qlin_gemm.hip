@@ -331,12 +331,16 @@ __global__ __launch_bounds__(128 * WN) void gemm_kernel(GemmParams p) {
     if constexpr (OUT != 2) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) sm[i] = p.s[min(mrow + 16 * i, p.M - 1)];
-        const int cmax = (SWIGLU ? ncols : p.Np) - 4;  // scales hold Np entries
+        // per element and clamped: with SwiGLU, N / 2 (the up block's first scale) may be
+        // any integer, so 16-byte loads would be misaligned
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int c = min(cbase + 16 * j, cmax);
-            sg[j] = *reinterpret_cast<const float4*>(p.wscale + c);
-            if constexpr (SWIGLU) su[j] = *reinterpret_cast<const float4*>(p.wscale + (p.N >> 1) + c);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = min(cbase + 16 * j + r, ncols - 1);
+                sg[j][r] = p.wscale[c];
+                if constexpr (SWIGLU) su[j][r] = p.wscale[(p.N >> 1) + c];
+            }
         }
     }
 

@@ -970,7 +970,8 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
     switch (waves) {
         case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4>(p, grid, items, lds, st);
         case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8>(p, grid, items, lds, st);
-        default: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
+        case 16: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
+        default: return hipErrorInvalidValue;  // the LDS above was sized for `waves`
     }
 }
 
@@ -991,7 +992,9 @@ static hipError_t launch_b(const GemvParams& p, int waves, size_t lds, hipStream
 
 hipError_t launch_gemv(const GemvParams& p, int bits, int waves, hipStream_t stream) {
     const bool fused = p.A != nullptr;
-    if (p.iw < 1 || p.iw > 16) return hipErrorInvalidValue;
+    if (p.iw < 1 || p.iw > 16 || (waves != 4 && waves != 8 && waves != 16)) return hipErrorInvalidValue;
+    // a fused prologue holds the rows in registers: refuse a wave count that cannot
+    if (fused && !gemv_can_fuse(p.M, p.K, waves, p.gamma != nullptr)) return hipErrorInvalidValue;
     const int groups = gemv_items(p);
     const int grid = p.grid > 0 && p.grid < groups ? p.grid : groups;
     const int items = (groups + grid - 1) / grid;

@@ -9,6 +9,9 @@
 // The replaced library stage is the CPU scan + quantize of rk_npu_w4a8_quant.cpp
 // (QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:26-27); the arithmetic is the oracle's,
 // src/npu.rs:1101-1110.
+#include <algorithm>
+#include <type_traits>
+
 #include "qlin_rows.hpp"
 
 namespace qlin {
@@ -353,6 +356,59 @@ hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream) {
             hipLaunchKernelGGL((quant_rows_kernel<float, false>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
+}
+
+// SiLU-gate on the unfused layout: Y[m, j] = SiLU(X[m, j]) * X[m, F + j] for j < F, the
+// gate block then the up block of each row (src/model/cpu.rs:119-152,327-351, Cpu::swiglu,
+// the reference's fallback when run_swiglu declines).  The same silu_gate as the fused
+// epilogues, so a caller that takes this route gets the fused path's bits.  Eight outputs
+// per thread when the strides and bases allow 16-byte fp16 / 32-byte f32 accesses.
+template <typename TY>
+__device__ __forceinline__ TY swiglu_out(float v) {
+    if constexpr (std::is_same<TY, _Float16>::value) return f16_of_f32(v);  // f32 result, then RNE to fp16
+    else return v;
+}
+
+template <typename TX, typename TY>
+__global__ void swiglu_kernel(int rows, int F, const TX* __restrict__ X, int64_t ldx, TY* __restrict__ Y, int64_t ldy,
+                              int vec) {
+    const int per = vec ? 8 : 1;
+    const int64_t chunks = (F + per - 1) / per;
+    const int64_t total = (int64_t)rows * chunks;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int m = (int)(i / chunks);
+        const int j0 = (int)(i - (int64_t)m * chunks) * per;
+        const TX* g = X + (int64_t)m * ldx + j0;
+        const TX* u = g + F;
+        TY* y = Y + (int64_t)m * ldy + j0;
+        if (vec && j0 + 8 <= F) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = swiglu_out<TY>(silu_gate((float)g[e], (float)u[e]));
+        } else {
+            for (int e = 0; e < per && j0 + e < F; ++e) y[e] = swiglu_out<TY>(silu_gate((float)g[e], (float)u[e]));
+        }
+    }
+}
+
+template <typename TX, typename TY>
+static hipError_t launch_swiglu_t(int rows, int F, const void* X, int64_t ldx, void* Y, int64_t ldy, hipStream_t st) {
+    const bool vec = F % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(X) & 31) == 0 &&
+                     (reinterpret_cast<uintptr_t>(Y) & 31) == 0;
+    const int64_t work = (int64_t)rows * (vec ? F / 8 : F);
+    const int grid = (int)std::min<int64_t>((work + 255) / 256, 4096);
+    hipLaunchKernelGGL((swiglu_kernel<TX, TY>), dim3(grid), dim3(256), 0, st, rows, F,
+                       reinterpret_cast<const TX*>(X), ldx, reinterpret_cast<TY*>(Y), ldy, vec ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(int rows, int F, const void* X, int x_f16, int64_t ldx, void* Y, int y_f16, int64_t ldy,
+                         hipStream_t st) {
+    if (x_f16) {
+        return y_f16 ? launch_swiglu_t<_Float16, _Float16>(rows, F, X, ldx, Y, ldy, st)
+                     : launch_swiglu_t<_Float16, float>(rows, F, X, ldx, Y, ldy, st);
+    }
+    return y_f16 ? launch_swiglu_t<float, _Float16>(rows, F, X, ldx, Y, ldy, st)
+                 : launch_swiglu_t<float, float>(rows, F, X, ldx, Y, ldy, st);
 }
 
 }  // namespace qlin

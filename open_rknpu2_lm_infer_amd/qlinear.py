@@ -12,7 +12,8 @@ import torch
 
 from . import _lib
 from ._lib import (QLIN_F16, QLIN_F32, QLIN_NO_FUSED_QUANT, QLIN_NORM_SEQUENTIAL,  # noqa: F401
-                   QLIN_RESIDUAL, QLIN_ROUND_HALF_EVEN, QLIN_SWIGLU, check)
+                   QLIN_PATH_GEMM, QLIN_PATH_GEMV, QLIN_PATH_GEMV_FUSED, QLIN_RESIDUAL, QLIN_ROUND_HALF_EVEN,
+                   QLIN_SWIGLU, check)
 
 _DT = {torch.float32: QLIN_F32, torch.float16: QLIN_F16}
 
@@ -80,7 +81,7 @@ class Workspace:
         self.handle = ctypes.c_void_p()
         check(_lib.load().qlin_workspace_create(max_rows, max_k, max_n, ctypes.byref(self.handle)),
               "qlin_workspace_create")
-        self.max_rows = max_rows
+        self.max_rows, self.max_k, self.max_n = max_rows, max_k, max_n
 
     def status(self, clear: bool = True) -> int:
         return _lib.load().qlin_workspace_status(self.handle, int(clear))
@@ -154,6 +155,9 @@ class Chain:
     def status(self, clear: bool = True) -> int:
         return _lib.load().qlin_chain_status(self.handle, int(clear))
 
+    def set_wait_limit(self, polls: int) -> None:
+        check(_lib.load().qlin_chain_set_wait_limit(self.handle, polls), "qlin_chain_set_wait_limit")
+
     def close(self):
         if self.handle:
             _lib.load().qlin_chain_free(self.handle)
@@ -215,6 +219,27 @@ def run(ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor | None = N
                                 _ptr(out), _DT[out.dtype], out.stride(0), flags, _stream())
     check(rc, "qlin_run")
     return out
+
+
+def swiglu(X: torch.Tensor, out: torch.Tensor | None = None, out_dtype=torch.float16) -> torch.Tensor:
+    """Y[m, j] = SiLU(X[m, j]) * X[m, F + j] on the unfused [M, 2F] layout (qlin_swiglu)."""
+    M, F2 = X.shape
+    F = F2 // 2
+    if out is None:
+        out = torch.empty((M, F), dtype=out_dtype, device=X.device)
+    assert X.stride(1) == 1 and out.stride(1) == 1
+    check(_lib.load().qlin_swiglu(M, F, _ptr(X), _DT[X.dtype], X.stride(0), _ptr(out), _DT[out.dtype],
+                                  out.stride(0), _stream()), "qlin_swiglu")
+    return out
+
+
+def plan(ws: Workspace, w: Weights, A: torch.Tensor, flags: int = 0, gamma: torch.Tensor | None = None) -> dict:
+    """The launches qlin_run / qlin_run_rmsnorm would make for these arguments (qlin_run_plan)."""
+    out = _lib.Plan()
+    check(_lib.load().qlin_run_plan(ws.handle, w.handle, A.shape[0], _ptr(A), A.stride(0),
+                                    _ptr(gamma) if gamma is not None else None, flags, ctypes.byref(out)),
+          "qlin_run_plan")
+    return {f: getattr(out, f) for f, _ in _lib.Plan._fields_ if f != "reserved"}
 
 
 def quantize(A: torch.Tensor, ldq: int | None = None, gamma: torch.Tensor | None = None, eps: float = 1e-6,

@@ -81,6 +81,10 @@ def test_null_handles_rejected():
     assert L.qlin_workspace_create(0, 8, 8, ctypes.byref(h)) == _lib.QLIN_ERR_PARAM
     assert L.qlin_workspace_create(4, 8, 0, ctypes.byref(h)) == _lib.QLIN_ERR_PARAM
     assert L.qlin_quantize(0, 8, None, 0, 8, None, 0.0, None, 8, None, None, 0, None) == _lib.QLIN_ERR_PARAM
+    assert L.qlin_swiglu(0, 8, None, 0, 16, None, 0, 8, None) == _lib.QLIN_ERR_PARAM
+    assert L.qlin_swiglu(1, 8, None, 0, 16, None, 0, 8, None) == _lib.QLIN_ERR_PARAM
+    assert L.qlin_run_plan(None, None, 1, None, 8, None, 0, None) == _lib.QLIN_ERR_PARAM
+    assert L.qlin_chain_set_wait_limit(None, 0) == _lib.QLIN_ERR_PARAM
     L.qlin_weights_free(None)
     L.qlin_workspace_free(None)
 
@@ -91,3 +95,19 @@ def test_structs_match_header_sizes():
     assert ctypes.sizeof(_lib.WorkspaceInfo) == 24
     assert ctypes.sizeof(_lib.DeviceInfo) == 48
     assert ctypes.sizeof(_lib.ChainStage) == 48
+    assert ctypes.sizeof(_lib.Plan) == 48
+
+
+def test_static_archive_links_and_runs():
+    """libqlinear.a carries every declared entry point, and a C program linked against it
+    whole (the way the reference's build.rs links its native library, build.rs:13-67)
+    runs its argument checks without a GPU."""
+    import subprocess
+    here = os.path.join(ROOT, "open_rknpu2_lm_infer_amd")
+    syms = subprocess.run(["nm", "-g", "--defined-only", os.path.join(here, "libqlinear.a")], check=True,
+                          capture_output=True, text=True).stdout
+    defined = set(re.findall(r"\bT (qlin_\w+)", syms))
+    assert set(declared_functions()) <= defined, set(declared_functions()) - defined
+    exe = os.path.join(ROOT, "tests", "cpp", "_build", "static_link_test")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "static link ok" in r.stdout, (r.returncode, r.stdout, r.stderr)

@@ -201,3 +201,29 @@ def test_chain_nonfinite_status():
     assert chain.status(clear=True) == QLIN_ERR_NONFINITE
     assert chain.status() == 0
     chain.close()
+
+
+def test_chain_wait_give_up_and_recover(ws):
+    """A stage wait that gives up (forced from the host with a wait limit of zero polls:
+    every kernel still exits normally) is reported as QLIN_ERR_DEVICE by qlin_chain_status,
+    which also restarts the stage counters; the same chain then runs correctly again with
+    the default limit (src/model/dense.rs:398-540 stages, two layers)."""
+    gam = [synth.gamma(synth.HIDDEN, seed=940 + i).to(DEV) for i in range(4)]
+    s0, h0 = qwen_layer_stages(0, gam[:2])
+    s1, h1 = qwen_layer_stages(1, gam[2:])
+    stages = s0 + s1
+    chain = ql.Chain(stages, max_rows=1)
+    x = synth.activations(1, synth.HIDDEN, seed=945, device=DEV)
+    chain.set_wait_limit(0)
+    chain.run(x)
+    torch.cuda.synchronize()
+    assert chain.status() == ql._lib.QLIN_ERR_DEVICE
+    chain.set_wait_limit(1 << 22)
+    for _ in range(2):
+        y = chain.run(x)
+        torch.cuda.synchronize()
+        assert chain.status() == 0
+        check_against_single(ws, chain, stages, x, y, 1)
+    with pytest.raises(QlinError):
+        chain.set_wait_limit(-1)
+    chain.close()

@@ -23,16 +23,28 @@ def ws():
     w.close()
 
 
+def override_ws(ws, **env):
+    """A workspace like ws whose kernel-variant overrides are the QLIN_* values given
+    (a workspace reads the overrides once, when it is created)."""
+    for k, v in env.items():
+        os.environ[k] = str(v)
+    try:
+        return ql.Workspace(ws.max_rows, ws.max_k, ws.max_n)
+    finally:
+        for k in env:
+            del os.environ[k]
+
+
 def run_both(ws, w, A, **kw):
     """Output of the default launch and of the one-item-per-workgroup launch."""
     out = ql.run(ws, w, A, **kw)
     torch.cuda.synchronize()
-    os.environ["QLIN_GEMV_GRID"] = "0"
-    try:
-        ref = ql.run(ws, w, A, **kw)
-        torch.cuda.synchronize()
-    finally:
-        del os.environ["QLIN_GEMV_GRID"]
+    ws1 = override_ws(ws, QLIN_GEMV_GRID=0)
+    ref = ql.run(ws1, w, A, **kw)
+    torch.cuda.synchronize()
+    assert ql.plan(ws1, w, A, kw.get("flags", 0), kw.get("gamma"))["grid"] == ql.plan(ws1, w, A, kw.get("flags", 0),
+                                                                                      kw.get("gamma"))["items"]
+    ws1.close()
     return out, ref
 
 
@@ -88,12 +100,11 @@ def test_item_width_matches_oracle(oracle, ws, iw, bits, N, swiglu):
         A = synth.activations(M, K, seed=322 + M)
         ref = ql.run(ws, w, A.to(DEV), out_dtype=torch.float16, flags=flags | extra)
         torch.cuda.synchronize()
-        os.environ["QLIN_GEMV_ITEM_WIDTH"] = str(iw)
-        try:
-            out = ql.run(ws, w, A.to(DEV), out_dtype=torch.float16, flags=flags | extra)
-            torch.cuda.synchronize()
-        finally:
-            del os.environ["QLIN_GEMV_ITEM_WIDTH"]
+        ws1 = override_ws(ws, QLIN_GEMV_ITEM_WIDTH=iw)
+        assert ql.plan(ws1, w, A.to(DEV), flags | extra)["item_width"] == iw
+        out = ql.run(ws1, w, A.to(DEV), out_dtype=torch.float16, flags=flags | extra)
+        torch.cuda.synchronize()
+        ws1.close()
         assert np.array_equal(f16_bits(out), f16_bits(ref))
         check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, swiglu), swiglu, torch.float16)
     w.close()
@@ -103,9 +114,10 @@ def test_item_width_matches_oracle(oracle, ws, iw, bits, N, swiglu):
 @pytest.mark.parametrize("order", ["neon16", "seq"])
 @pytest.mark.parametrize("M", [2, 3, 4])
 def test_rmsnorm_rows_fused(oracle, ws, bits, order, M):
-    """RMSNorm of 2-4 rows inside the GEMV prologue (one wave per row sums its squares):
-    against the oracle, and bit for bit against the separate RMSNorm-quantize launch
-    (QLIN_NO_FUSED_QUANT) and the one-item-per-workgroup launch, fp16 and f32 rows."""
+    """RMSNorm of 2-4 rows inside the GEMV prologue (one wave per row sums its squares;
+    the launch plan confirms the fused path ran): against the oracle, and bit for bit
+    against the separate RMSNorm-quantize launch (QLIN_NO_FUSED_QUANT) and the
+    one-item-per-workgroup launch, fp16 and f32 rows."""
     K = 2560
     flags0 = ql.QLIN_NORM_SEQUENTIAL if order == "seq" else 0
     for N, swiglu in ((2 * 16 * 600, True), (16 * 300, False), (2560, False)):
@@ -122,6 +134,12 @@ def test_rmsnorm_rows_fused(oracle, ws, bits, order, M):
             expect = oracle.swiglu(expect)
         for dt in (torch.float16, torch.float32):
             a = A.to(DEV).to(dt)
+            # RMSNorm of 2-4 rows at K = 2560 runs inside the GEMV, except W8 N = 2560 at 4
+            # rows: its 16-wave workgroups cannot hold 4 normalized rows, and at 4 rows the
+            # separate launch is kept rather than fewer waves
+            fused = not (bits == 8 and N == 2560 and M == 4)
+            path = ql.plan(ws, w, a, flags, gam.to(DEV))["path"]
+            assert path == (ql.QLIN_PATH_GEMV_FUSED if fused else ql.QLIN_PATH_GEMV), (N, M, path)
             out, ref = run_both(ws, w, a, out_dtype=torch.float16, flags=flags, gamma=gam.to(DEV), eps=1e-6)
             sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags | ql.QLIN_NO_FUSED_QUANT,
                          gamma=gam.to(DEV), eps=1e-6)
@@ -147,8 +165,14 @@ def test_fused_rows_fewer_waves(oracle, bits, K, M):
     w = make_weights(bits, codes, sc)
     A = synth.activations(M, K, seed=332 + M)
     expect = oracle_linear(oracle, A, codes, sc, False)
+    # fused where 16-wave workgroups cannot hold the rows but fewer waves can: K = 4096 up
+    # to 3 rows, K = 9728 up to 2; 4 rows quantize in a separate launch there
+    fused = M <= (3 if K == 4096 else 2)
     for dt in (torch.float16, torch.float32):
         a = A.to(DEV).to(dt)
+        pl = ql.plan(ws, w, a)
+        assert pl["path"] == (ql.QLIN_PATH_GEMV_FUSED if fused else ql.QLIN_PATH_GEMV), pl
+        assert ql.plan(ws, w, a, ql.QLIN_NO_FUSED_QUANT)["path"] == ql.QLIN_PATH_GEMV
         out = ql.run(ws, w, a, out_dtype=torch.float16)
         sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=ql.QLIN_NO_FUSED_QUANT)
         torch.cuda.synchronize()

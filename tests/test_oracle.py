@@ -329,3 +329,84 @@ def test_golden_fixtures(oracle):
         q, s, acc, out = oracle.linear(inp, codes, scales)
         assert np.array_equal(acc, data[f"narrow_n{n}_acc"])
         assert np.array_equal(out.view(np.uint32), data[f"narrow_n{n}_out"].view(np.uint32))
+
+
+# ---------------------------------------------------------------- whole linear (the timed CPU baseline)
+
+
+def linear_f16_independent(A_bits, w_nk, scales, gamma=None, eps=1e-6, rne=False):
+    """oracle_linear_f16 by routes that share no code with it: numpy fp16 -> f32, the
+    exact-rational NEON-order RMSNorm scale, numpy quantization with exact rounding,
+    an int64 matmul, numpy f32 dequant; returns the f32 result before SwiGLU / fp16."""
+    x = A_bits.view(np.float16).astype(np.float32)
+    if gamma is not None:
+        rows = []
+        for r in range(x.shape[0]):
+            sc = neon16_scale_exact(x[r], eps)
+            rows.append((x[r] * sc).astype(np.float32) * gamma)
+        x = np.stack(rows).astype(np.float32)
+    q, s = quantize_independent(x, rne)
+    acc = q.astype(np.int64) @ w_nk.astype(np.int64).T
+    assert np.abs(acc).max() < 2 ** 31
+    return (acc.astype(np.float32) * s[:, None]).astype(np.float32) * scales[None, :]
+
+
+@pytest.mark.parametrize("bits,M,K,N,use_gamma,swiglu,rne,threads", [
+    (4, 3, 2560, 128, False, False, False, 1),
+    (8, 2, 2560, 96, True, False, False, 4),
+    (4, 5, 333, 64, True, True, False, 3),
+    (8, 4, 512, 200, False, True, True, 2),
+    (4, 1, 16, 2, True, False, True, 1),
+])
+def test_linear_f16_matches_independent_route(oracle, bits, M, K, N, use_gamma, swiglu, rne, threads):
+    """oracle_linear_f16 (src/npu.rs:1097-1121, 1202-1208; src/model/cpu.rs:11-66): bit-exact
+    against the independent route for the plain output, and for SwiGLU bit-exact against the
+    pinned oracle_swiglu of that route plus 1e-6 of float64 x*sigmoid(x)*u."""
+    rng = np.random.default_rng(1000 + M * K + N)
+    lo, hi = (-8, 7) if bits == 4 else (-127, 127)
+    w_nk = rng.integers(lo, hi + 1, size=(N, K)).astype(np.int8)
+    sc = rng.uniform(0.01, 0.1, N).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, rng.choice(K, max(1, K // 100), replace=False)] *= 20
+    if K >= 8:
+        x[0, :4] = [127.0, 2.5, -2.5, 0.5]  # ties when s lands on 1
+    A = x.astype(np.float16).view(np.uint16)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16).astype(np.float32) if use_gamma else None
+    got = oracle.linear_f16(A, w_nk, sc, swiglu=swiglu, gamma=gamma, eps=1e-6,
+                            round_mode=oracle.ROUND_EVEN if rne else oracle.ROUND_AWAY, threads=threads)
+    y = linear_f16_independent(A, w_nk, sc, gamma, 1e-6, rne)
+    if not swiglu:
+        assert np.array_equal(got, y.astype(np.float16).view(np.uint16))
+        return
+    mid = oracle.swiglu(y)
+    assert np.array_equal(got, mid.astype(np.float16).view(np.uint16))
+    g, u = y[:, :N // 2].astype(np.float64), y[:, N // 2:].astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    assert np.allclose(mid, ref, rtol=1e-6, atol=1e-30)
+
+
+def test_linear_f16_catches_planted_mistakes(oracle):
+    """The route above tells apart the mistakes a restatement could make: swapped gate and
+    up halves, a dropped RMSNorm weight, and the other rounding mode on exact ties (the
+    dequant grouping is pinned at f32 by test_dequant_order)."""
+    rng = np.random.default_rng(77)
+    M, K, N = 2, 256, 64
+    w_nk = rng.integers(-8, 8, size=(N, K)).astype(np.int8)
+    sc = rng.uniform(0.01, 0.1, N).astype(np.float32)
+    A = rng.standard_normal((M, K)).astype(np.float16).view(np.uint16)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float32)
+    y = linear_f16_independent(A, w_nk, sc, gamma)
+    got = oracle.linear_f16(A, w_nk, sc, swiglu=True, gamma=gamma)
+    swapped = oracle.swiglu(np.concatenate([y[:, N // 2:], y[:, :N // 2]], axis=1))
+    assert not np.array_equal(got, swapped.astype(np.float16).view(np.uint16))
+    no_gamma = oracle.swiglu(linear_f16_independent(A, w_nk, sc, None))
+    assert not np.array_equal(got, no_gamma.astype(np.float16).view(np.uint16))
+    # absmax 127 -> s = 1: every x = j + 0.5 is a tie that the two modes round apart
+    x = np.zeros((1, K), np.float32)
+    x[0, 0] = 127
+    x[0, 1:] = (np.arange(K - 1) % 50) + 0.5
+    At = x.astype(np.float16).view(np.uint16)
+    away = oracle.linear_f16(At, w_nk, sc)
+    assert np.array_equal(away, linear_f16_independent(At, w_nk, sc).astype(np.float16).view(np.uint16))
+    even = linear_f16_independent(At, w_nk, sc, rne=True).astype(np.float16).view(np.uint16)
+    assert not np.array_equal(away, even)
