@@ -198,6 +198,20 @@ int qlin_run_residual(qlin_workspace* ws, const qlin_weights* weights, int32_t r
                       int32_t a_dtype, int64_t lda, const void* R, int32_t r_dtype, int64_t ldr,
                       float multiplier, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags, void* stream);
 
+/* qlin_run_rmsnorm (gamma != NULL) or qlin_run (gamma == NULL) without a workspace: no
+ * counterpart in the reference.  For callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): it calls no hipMalloc,
+ * hipFree or allocating routine.  Its scratch (quantized rows, per-token scales, split-K
+ * partial sums and counters) is a 32.05 MiB static device array that each GPU the library
+ * runs on holds until the process ends; every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU race (run them on one stream).  The first call on a device
+ * also clears that array's counters with a kernel on `stream`.  Limits: rows <= 4096 and
+ * rows * K_padded <= 16 MiB, else QLIN_ERR_UNSUPPORTED.  err (device uint32, may be NULL)
+ * gets bit 0 set when an activation row holds Inf/NaN.  Otherwise as qlin_run_rmsnorm. */
+int qlin_run_noalloc(const qlin_weights* weights, int32_t rows, const void* A, int32_t a_dtype, int64_t lda,
+                     const float* gamma, float eps, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags,
+                     uint32_t* err, void* stream);
+
 /* ---- stage entry points (parity checks and composition) ----
  * Per-token quantization alone (the library's scan + quantize,
  * QWEN3_W4A8_PIPELINE_REVIEW_20261020.md:26-27).  q: device int8 [rows, ldq], the

@@ -76,6 +76,7 @@ SIGNATURES = {
     "qlin_chain_stage_output": (ctypes.c_int, [_P, _I32, _P, _P]),
     "qlin_chain_status": (ctypes.c_int, [_P, _I32]),
     "qlin_chain_set_wait_limit": (ctypes.c_int, [_P, _I32]),
+    "qlin_run_noalloc": (ctypes.c_int, [_P, _I32, _P, _I32, _I64, _P, _F, _P, _I32, _I64, _U32, _P, _P]),
     "qlin_swiglu": (ctypes.c_int, [_I32, _I32, _P, _I32, _I64, _P, _I32, _I64, _P]),
     "qlin_run_plan": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _P, _U32, _P]),
 }

@@ -49,7 +49,8 @@ struct qlin_workspace {
     float* s;            // [max_rows]
     uint32_t* counters;  // [n_counters], zero at rest
     int n_counters;
-    int32_t* gemm_part;  // [kGemmPartInts]
+    int32_t* gemm_part;  // [part_ints]
+    int64_t part_ints;   // capacity of gemm_part (ints)
     uint32_t* err;       // sticky error word
     float* dA;           // host-API staging [max_rows, max_k]
     float* dC;           // host-API staging [max_rows, max_n]
@@ -436,6 +437,7 @@ int qlin_workspace_create(int32_t max_rows, int32_t max_k, int32_t max_n, qlin_w
     ws->device = dev;
     ws->cu_count = cu_count(dev);
     ws->ov = read_overrides();
+    ws->part_ints = kGemmPartInts;
     ws->n_counters = std::max(ws->max_np / 16, 8192);
     const size_t bq = (size_t)max_rows * ws->max_kp, bs = (size_t)max_rows * sizeof(float);
     const size_t bc = (size_t)ws->n_counters * sizeof(uint32_t);
@@ -650,7 +652,7 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
         S = std::min(S, std::max(1, ktiles / 4));
     }
     S = std::max(1, std::min(S, ktiles));
-    while (S > 1 && ((int64_t)tiles * S * slice > kGemmPartInts || tiles > ws->n_counters)) --S;
+    while (S > 1 && ((int64_t)tiles * S * slice > ws->part_ints || tiles > ws->n_counters)) --S;
     // the GEMM's k loop takes two tiles per iteration: Kp is a multiple of 256, so
     // ktiles is even, and an even split size keeps every split's count even
     if (ktiles % 2) return QLIN_ERR_PARAM;
@@ -877,6 +879,110 @@ int qlin_swiglu(int32_t rows, int32_t F, const void* X, int32_t x_dtype, int64_t
 }
 
 }  // extern "C"
+
+// ---- runs without a workspace: scratch in a static device array --------------------
+//
+// qlin_run_noalloc serves callers that cannot allocate (code under HIP graph capture,
+// tight serving loops).  Its scratch lives in `scratch`, a file-scope device array of
+// kScratchBytes (32.05 MiB) that every GPU the library runs on holds until the process
+// ends.  Layout: the error word, the split-K tile counters (zero at rest: the GEMM's
+// last workgroup per tile re-zeroes its counter), the per-token scales, the quantized
+// rows, the split-K partial sums.  In host code `scratch` names a host-side stand-in,
+// not device memory: its device address is looked up once per device with
+// hipGetSymbolAddress, and only that address is passed to kernels.
+
+namespace {
+
+constexpr size_t kNaErr = 0;                                   // uint32 error word (256 B)
+constexpr int kNaCounters = 8192;                              // split-K tile counters
+constexpr size_t kNaCountersOff = 256;
+constexpr int kNaMaxRows = 4096;                               // rows per call
+constexpr size_t kNaScalesOff = kNaCountersOff + kNaCounters * 4;          // 33,024
+constexpr size_t kNaQOff = (kNaScalesOff + kNaMaxRows * 4 + 255) / 256 * 256;  // 49,408
+constexpr size_t kNaQBytes = (size_t)16 << 20;                 // rows x K_padded <= 16 MiB
+constexpr size_t kNaPartOff = kNaQOff + kNaQBytes;
+constexpr int64_t kNaPartInts = (int64_t)4 << 20;              // 16 MiB of split-K partials
+constexpr size_t kScratchBytes = kNaPartOff + (size_t)kNaPartInts * 4;
+static_assert(kNaPartOff % 256 == 0 && kNaQOff % 256 == 0, "scratch regions stay 256-byte aligned");
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+constexpr int kNaMaxDevices = 64;
+struct NoAllocDevice {
+    std::atomic<uint8_t*> ptr{nullptr};  // device address of `scratch` on this device
+    int cu_count = 0;
+    QlinOverrides ov{};
+};
+NoAllocDevice g_noalloc[kNaMaxDevices];
+std::mutex g_noalloc_mutex;
+
+// Device address of this device's `scratch` (the current device must be `dev`).  The first
+// call on a device looks it up and clears the error word and counters with a fill kernel on
+// `st` (a kernel rather than a memset node, should the caller be capturing a graph).
+int noalloc_scratch(int dev, hipStream_t st, uint8_t** out) {
+    if (dev < 0 || dev >= kNaMaxDevices) return QLIN_ERR_NODEVICE;
+    uint8_t* p = g_noalloc[dev].ptr.load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> g(g_noalloc_mutex);
+        p = g_noalloc[dev].ptr.load(std::memory_order_relaxed);
+        if (!p) {
+            void* sym = nullptr;
+            if (hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch)) != hipSuccess || !sym) return QLIN_ERR_DEVICE;
+            uint8_t* base = static_cast<uint8_t*>(sym);
+            const int words = (int)(kNaScalesOff / 4);  // the error word's block and the counters
+            hipLaunchKernelGGL(zero_words_kernel, dim3(32), dim3(256), 0, st, reinterpret_cast<uint32_t*>(base), words);
+            if (hipGetLastError() != hipSuccess) return QLIN_ERR_DEVICE;
+            g_noalloc[dev].cu_count = cu_count(dev);
+            g_noalloc[dev].ov = read_overrides();
+            g_noalloc[dev].ptr.store(base, std::memory_order_release);
+            p = base;
+        }
+    }
+    *out = p;
+    return QLIN_OK;
+}
+
+}  // namespace
+
+extern "C" int qlin_run_noalloc(const qlin_weights* w, int32_t rows, const void* A, int32_t a_dtype, int64_t lda,
+                                const float* gamma, float eps, void* C, int32_t c_dtype, int64_t ldc, uint32_t flags,
+                                uint32_t* err, void* stream) {
+    if (!w || rows <= 0) return QLIN_ERR_PARAM;
+    if (rows > kNaMaxRows || (int64_t)rows * w->Kp > (int64_t)kNaQBytes) return QLIN_ERR_UNSUPPORTED;
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    if (dev != w->device) return QLIN_ERR_PARAM;
+    const hipStream_t st = (hipStream_t)stream;
+    uint8_t* base = nullptr;
+    if (int rc = noalloc_scratch(dev, st, &base)) return rc;
+    // a workspace on the stack whose every buffer is a region of `scratch`
+    qlin_workspace ws{};
+    ws.max_rows = kNaMaxRows;
+    ws.max_k = w->K;
+    ws.max_n = w->N;
+    ws.max_kp = w->Kp;
+    ws.max_np = w->Np;
+    ws.device = dev;
+    ws.cu_count = g_noalloc[dev].cu_count;
+    ws.ov = g_noalloc[dev].ov;
+    ws.q = reinterpret_cast<int8_t*>(base + kNaQOff);
+    ws.s = reinterpret_cast<float*>(base + kNaScalesOff);
+    ws.counters = reinterpret_cast<uint32_t*>(base + kNaCountersOff);
+    ws.n_counters = kNaCounters;
+    ws.gemm_part = reinterpret_cast<int32_t*>(base + kNaPartOff);
+    ws.part_ints = kNaPartInts;
+    ws.err = err ? err : reinterpret_cast<uint32_t*>(base + kNaErr);
+    ws.last = st;
+    return run_impl(&ws, w, rows, A, a_dtype, lda, gamma, eps, C, c_dtype, ldc, flags, st);
+}
 
 // ---- decode chain --------------------------------------------------------------
 
