@@ -40,6 +40,8 @@ struct QlinOverrides {
     int gemm_group_m;     // QLIN_GEMM_GROUP_M (default 4)
     int gemm_deep;        // QLIN_GEMM_DEEP, 0 / 1
     int gemm_wn;          // QLIN_GEMM_WN, 2 / 4
+    int gemm_kernel;      // QLIN_GEMM_KERNEL: 16 forces the 16x16x64 kernel
+    int gemm_cfg;         // QLIN_GEMM_CFG: forces the 32x32x32 kernel with tile configuration 0..2
 };
 
 struct qlin_workspace {
@@ -82,6 +84,8 @@ QlinOverrides read_overrides() {
     o.gemm_group_m = env_int("QLIN_GEMM_GROUP_M", 4);
     o.gemm_deep = env_int("QLIN_GEMM_DEEP", -1);
     o.gemm_wn = env_int("QLIN_GEMM_WN", 4);
+    o.gemm_kernel = env_int("QLIN_GEMM_KERNEL", 0);
+    o.gemm_cfg = env_int("QLIN_GEMM_CFG", -1);
     return o;
 }
 
@@ -627,20 +631,53 @@ int run_gemv(qlin_workspace* ws, const qlin_weights* w, int rows, const void* A,
 
 // Launch shape of a prefill GEMM.
 struct GemmPlan {
-    int bn, m_tiles, n_tiles, splits, ktiles_per_split, group_m, deep, wn;
+    int kernel;  // 32: the 32x32x32 kernel (tile configuration cfg), 16: the 16x16x64 kernel
+    int cfg, bm, bn, threads;
+    int m_tiles, n_tiles, splits, ktiles_per_split, group_m, deep, wn;
 };
+
+// Kernel and tile configuration for a shape.  Measured (MI355X, four Qwen3-4B linears, M = 512
+// and 4096, fp16 out): the 32x32x32 kernel's 256 x 256 tile is ahead only where it leaves
+// every CU several tiles (M = 4096 gate_up: 194-206 vs 212-227 us); with one round or less
+// the 16x16x64 kernel is equal or ahead (M = 512: the 128 x 128 tiles of both run at the
+// same copy rate, ~20 B per clock per CU), so it stays the default there.
+// Returns -1 for the 16x16x64 kernel, else the 32x32x32 tile configuration.
+int gemm_pick(const qlin_workspace* ws, const qlin_weights* w, int rows, bool sw) {
+    if (ws->ov.gemm_kernel == 16) return -1;
+    if (ws->ov.gemm_cfg >= 0 && ws->ov.gemm_cfg <= 2) return ws->ov.gemm_cfg;
+    if (w->bits != 4) return -1;
+    const GemmTileCfg big = gemm32_tile(w->bits, 1);
+    const int cols = sw ? w->N / 2 : w->N, bcols = sw ? big.bn / 2 : big.bn;
+    const int64_t big_tiles = (int64_t)((rows + big.bm - 1) / big.bm) * ((cols + bcols - 1) / bcols);
+    return big_tiles >= 4 * ws->cu_count ? 1 : -1;
+}
 
 int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags, GemmPlan* out) {
     const QlinOverrides& ov = ws->ov;
     const bool sw = (flags & kFlagSwiglu) != 0;
     GemmPlan g{};
-    g.bn = gemm_tile_n(w->bits, w->N);
+    const int pick = gemm_pick(ws, w, rows, sw);
+    g.kernel = pick < 0 ? 16 : 32;
+    int64_t slice;  // ints of one partial tile
+    if (g.kernel == 32) {
+        g.cfg = pick;
+        const GemmTileCfg t = gemm32_tile(w->bits, g.cfg);
+        g.bm = t.bm;
+        g.bn = t.bn;
+        g.threads = t.threads;
+        slice = (int64_t)t.regs * t.threads;
+    } else {
+        g.bm = kGemmTileM;
+        g.bn = gemm_tile_n(w->bits, w->N);
+        g.wn = ov.gemm_wn == 2 ? 2 : 4;  // 2 x 4 waves unless QLIN_GEMM_WN=2
+        g.threads = 128 * g.wn;
+        slice = (int64_t)gemm_regs_per_thread(g.bn) * 256;
+    }
     const int cols = sw ? g.bn / 2 : g.bn;  // output channels per tile
-    g.m_tiles = (rows + kGemmTileM - 1) / kGemmTileM;
+    g.m_tiles = (rows + g.bm - 1) / g.bm;
     g.n_tiles = ((sw ? w->N / 2 : w->N) + cols - 1) / cols;
     const int ktiles = w->Kp / kGemmTileK;
     const int tiles = g.m_tiles * g.n_tiles;
-    const int64_t slice = (int64_t)gemm_regs_per_thread(g.bn) * 256;  // ints of one partial tile
     int S = ov.gemm_splits;
     if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
     if (S <= 0) {
@@ -653,15 +690,14 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
     }
     S = std::max(1, std::min(S, ktiles));
     while (S > 1 && ((int64_t)tiles * S * slice > ws->part_ints || tiles > ws->n_counters)) --S;
-    // the GEMM's k loop takes two tiles per iteration: Kp is a multiple of 256, so
-    // ktiles is even, and an even split size keeps every split's count even
+    // the 16x16x64 kernel's k loop takes two tiles per iteration: Kp is a multiple of 256,
+    // so ktiles is even, and an even split size keeps every split's count even
     if (ktiles % 2) return QLIN_ERR_PARAM;
     g.ktiles_per_split = ((ktiles + S - 1) / S + 1) & ~1;
     g.splits = (ktiles + g.ktiles_per_split - 1) / g.ktiles_per_split;
     g.group_m = std::max(1, std::min(g.m_tiles, ov.gemm_group_m));
     // a grid with at most one workgroup per CU takes the deeper pipeline
     g.deep = ov.gemm_deep >= 0 ? (ov.gemm_deep != 0) : (int64_t)tiles * g.splits <= ws->cu_count;
-    g.wn = ov.gemm_wn == 2 ? 2 : 4;  // 2 x 4 waves unless QLIN_GEMM_WN=2
     *out = g;
     return QLIN_OK;
 }
@@ -701,7 +737,8 @@ int run_gemm(qlin_workspace* ws, const qlin_weights* w, int rows, const int8_t* 
     p.counters = ws->counters;
     p.deep = g.deep;
     p.wn = g.wn;
-    return launch_gemm(p, w->bits, g.bn, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
+    const hipError_t e = g.kernel == 32 ? launch_gemm32(p, w->bits, g.cfg, st) : launch_gemm(p, w->bits, g.bn, st);
+    return e == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
 }
 
 int check_run(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags) {
@@ -858,8 +895,8 @@ int qlin_run_plan(const qlin_workspace* ws, const qlin_weights* w, int32_t rows,
     GemmPlan g;
     if (int rc = plan_gemm(ws, w, rows, flags, &g)) return rc;
     out->path = QLIN_PATH_GEMM;
-    out->waves = 2 * g.wn;
-    out->tile_m = kGemmTileM;
+    out->waves = g.threads / 64;
+    out->tile_m = g.bm;
     out->tile_n = (flags & kFlagSwiglu) ? g.bn / 2 : g.bn;
     out->items = g.m_tiles * g.n_tiles;
     out->splits = g.splits;

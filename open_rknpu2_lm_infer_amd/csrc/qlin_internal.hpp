@@ -128,6 +128,12 @@ size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm
 hipError_t launch_gemm(const GemmParams& p, int bits, int bn, hipStream_t stream);
 int gemm_tile_n(int bits, int N);          // channels of B per workgroup tile
 int gemm_regs_per_thread(int bn);          // int32 accumulators per thread of one tile
+// Tile of the 32x32x32 GEMM: tokens x weight rows, threads, int32 accumulators per thread.
+struct GemmTileCfg {
+    int bm, bn, threads, regs;
+};
+GemmTileCfg gemm32_tile(int bits, int cfg);
+hipError_t launch_gemm32(const GemmParams& p, int bits, int cfg, hipStream_t stream);
 hipError_t launch_swiglu(int rows, int F, const void* X, int x_f16, int64_t ldx, void* Y, int y_f16, int64_t ldy,
                          hipStream_t stream);
 hipError_t launch_pack_w4(const int8_t* codes_nk, int N, int K, int Np, int Kp, uint8_t* out,
