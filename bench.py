@@ -7,17 +7,21 @@ decoder layer's four projections (qkv 2560->6144, o 4096->2560, gate_up
 byte.  One step = those four linears of one layer, each a single launch that
 quantizes its fp16 input row itself.  The steps rotate over 36 distinct layer copies
 (1.82 GB of weights), so the 256 MB Infinity Cache cannot hold the stream.
-Bytes per step = packed codes + f32 scales = 50,585,600.
+Bytes per step = packed codes + f32 scales = 50,585,600.  Exactly --steps steps are
+timed (whole 36-layer graphs plus one graph of the remainder), between HIP events on
+the launch stream; the per-step distribution (median, p10, p90) comes from at least
+100 separately timed 36-layer graph replays.
 
-Also reported: the dominant kernel's roofline (the gate_up GEMV, HIP events on the
-launch stream), int8 TOPS of the M=512 prefill GEMMs of the same layer, the 36-layer
-mixed W4/W8 stack at M=1 and M=4 (RMSNorm before qkv and gate_up, one launch per
-linear and the one-launch decode chain), the M=4096 prefill layer with RMSNorm fused
-into the quantization of qkv and gate_up (Student-t activations), and the CPU oracle
-timed on the host cores over a bounded sample of the same workload.
+Also reported: the dominant kernel's roofline (the gate_up GEMV), the W8 GEMV at
+M=1 K=N=2560 (its own line, >= 512 MB of rotated copies), int8 TOPS of the M=512
+prefill linears with the roofline of the dominant GEMM kernel, the 36-layer mixed
+W4/W8 stack at M=1 and M=4 (one launch per linear and the one-launch decode chain),
+the W8 lm_head, the M=4096 prefill layer with RMSNorm fused into the quantization
+(Student-t activations), and the CPU oracle on the host cores over a bounded sample.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--prefill-reps R]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
     python bench.py --mode kernel   # only the dominant kernel, for rocprofv3 --pmc passes
+    python bench.py --mode gemm     # only the M=512 GEMMs, for rocprofv3 --pmc passes
     python bench.py --mode copy     # a plain 256 MiB device copy, the counters' calibration
 
 roofline.traffic is read from profiles/gemv_gate_up_w4_m1_traffic.txt (written by
@@ -28,12 +32,14 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published (5.0 POPS)
+ROTATE_BYTES = 512 << 20     # per-kernel measurements rotate at least this many weight bytes
 
 
 def log(msg):
@@ -52,17 +58,27 @@ def read_traffic():
     return None
 
 
+def pct(xs, q):
+    xs = sorted(xs)
+    if not xs:
+        return None
+    i = (len(xs) - 1) * q / 100.0
+    lo, hi = int(math.floor(i)), int(math.ceil(i))
+    return xs[lo] + (xs[hi] - xs[lo]) * (i - lo)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=2016)
+    ap.add_argument("--warmup", type=int, default=216)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--kernel-reps", type=int, default=1000)
+    ap.add_argument("--replays", type=int, default=120, help="36-layer graph replays timed one by one")
+    ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "kernel", "copy"], default="full")
+    ap.add_argument("--mode", choices=["full", "kernel", "gemm", "copy"], default="full")
     ap.add_argument("--stack-reps", type=int, default=5)
     ap.add_argument("--long-reps", type=int, default=3)
     ap.add_argument("--no-stack", action="store_true")
@@ -74,6 +90,8 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded "
               "across GPUs in this build.", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1:
+        sys.exit("--steps must be >= 1")
 
     import numpy as np
     import torch
@@ -97,9 +115,36 @@ def main():
     info = _lib.device_info(0)
     log(f"device: {torch.cuda.get_device_name(0)} CUs={info.cu_count} sclk={info.sclk_khz / 1e3:.0f} MHz")
 
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def capture(fn, count, start=0):
+        """HIP graph of fn(start..start+count-1); launches happen on torch's capture stream."""
+        for i in range(min(count, 4)):
+            fn(start + i)  # eager first: code objects load outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(count):
+                fn(start + i)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, reps):
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3  # seconds
+
     # ---------------------------------------------------------------- weights (resident)
     L = args.layers
-    only = [p for p, (n, _, _) in enumerate(synth.LAYER) if n == "gate_up"] if args.mode == "kernel" else None
+    only = None
+    if args.mode == "kernel":
+        only = [p for p, (n, _, _) in enumerate(synth.LAYER) if n == "gate_up"]
     layers = []
     codes0 = []  # host copy of layer 0 for the CPU baseline
     t0 = time.time()
@@ -126,36 +171,6 @@ def main():
             for name, K, N in synth.LAYER]
     flags = [ql.QLIN_SWIGLU if name == "gate_up" else 0 for name, _, _ in synth.LAYER]
 
-    def step(i):
-        projs = layers[i % L]
-        for p in range(4):
-            ql.run(ws, projs[p], acts[p], out=outs[p], flags=flags[p])
-
-    st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-    def capture(fn, count):
-        """HIP graph of fn(0..count-1); launches happen on torch's capture stream."""
-        for i in range(min(count, 4)):
-            fn(i)  # eager first: code objects load outside the capture
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(count):
-                fn(i)
-        torch.cuda.synchronize()
-        return g
-
-    def time_graph(g, reps):
-        g.replay()
-        torch.cuda.synchronize()
-        e0.record(st)
-        for _ in range(reps):
-            g.replay()
-        e1.record(st)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e-3  # seconds
-
     if args.mode == "kernel":
         p = only[0]
         g = capture(lambda i: ql.run(ws, layers[i % L][p], acts[p], out=outs[p], flags=flags[p]), L)
@@ -163,63 +178,161 @@ def main():
         log(f"gate_up gemv: {sec * 1e6 / (10 * L):.2f} us/launch over {10 * L} launches")
         return
 
+    M512 = 512
+    pre_acts = [synth.activations(M512, K, seed=synth.linear_seed(0, p) + 2, device=dev)
+                for p, (_, K, _) in enumerate(synth.LAYER)]
+    pre_outs = [torch.empty((M512, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+                for name, K, N in synth.LAYER]
+    pre_q = []
+    for p, (_, K, _) in enumerate(synth.LAYER):
+        pre_q.append(ql.quantize(pre_acts[p], ldq=layers[0][p].K_padded))
+    torch.cuda.synchronize()
+
+    def gemm_only(p, i):
+        q, s = pre_q[p]
+        lib = _lib.load()
+        w = layers[i % L][p]
+        ql.check(lib.qlin_run_quantized(ws.handle, w.handle, M512, ql._ptr(q), q.stride(0), ql._ptr(s),
+                                        ql._ptr(pre_outs[p]), ql.QLIN_F16, pre_outs[p].stride(0), flags[p],
+                                        ql._stream()), "qlin_run_quantized")
+
+    if args.mode == "gemm":
+        for p in range(4):
+            for i in range(L):
+                gemm_only(p, i)
+        torch.cuda.synchronize()
+        log("M=512 GEMMs done")
+        return
+
     # ---------------------------------------------------------------- headline: decode layer
-    # One graph = one pass over the L resident layers (4 launches each); the timed
-    # region replays it until `steps` layer-steps have run.
+    def step(i):
+        projs = layers[i % L]
+        for p in range(4):
+            ql.run(ws, projs[p], acts[p], out=outs[p], flags=flags[p])
+
     g_layers = capture(step, L)
-    reps_w = max(1, -(-args.warmup // L))
-    time_graph(g_layers, reps_w)
-    log(f"warmup {reps_w * L} steps done")
-    reps = max(1, -(-args.steps // L))
-    steps = reps * L
+    rem = args.steps % L
+    g_rem = capture(step, rem) if rem else None
+    time_graph(g_layers, max(1, -(-args.warmup // L)))
+    log(f"warmup {max(1, -(-args.warmup // L)) * L} steps done")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    sec = time_graph(g_layers, reps)
-    wall = time.perf_counter() - t0
-    ms_per_step = sec * 1e3 / steps
-    value = bytes_layer * steps / sec / 1e9
-    log(f"decode layer (graph): {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s (wall {wall:.3f} s)")
-    # eager launches of the same step, for reference (host launch rate bound)
-    torch.cuda.synchronize()
     e0.record(st)
-    for i in range(200):
-        step(i)
+    for _ in range(args.steps // L):
+        g_layers.replay()
+    if g_rem is not None:
+        g_rem.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    eager_us = e0.elapsed_time(e1) * 1e3 / 200
-    log(f"decode layer (eager launches): {eager_us:.2f} us/step")
+    wall = time.perf_counter() - t0
+    sec = e0.elapsed_time(e1) * 1e-3
+    steps = args.steps
+    ms_per_step = sec * 1e3 / steps
+    value = bytes_layer * steps / sec / 1e9
+    log(f"decode layer (graph): {steps} steps, {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s (wall {wall:.3f} s)")
+    # per-step distribution: each 36-layer replay timed on its own
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.replays + 1)]
+    torch.cuda.synchronize()
+    evs[0].record(st)
+    for r in range(args.replays):
+        g_layers.replay()
+        evs[r + 1].record(st)
+    torch.cuda.synchronize()
+    per_step = [evs[r].elapsed_time(evs[r + 1]) * 1e3 / L for r in range(args.replays)]
+    dist = {"replays": args.replays, "steps_per_replay": L, "median_us": round(pct(per_step, 50), 3),
+            "p10_us": round(pct(per_step, 10), 3), "p90_us": round(pct(per_step, 90), 3)}
+    log(f"decode layer per-step: median {dist['median_us']} us, p10 {dist['p10_us']}, p90 {dist['p90_us']}")
+    # eager launches of the same step through pre-bound C-ABI calls
+    bound = [[ql.BoundRun(ws, layers[l][p], acts[p], outs[p], flags[p]) for p in range(4)] for l in range(L)]
+    for l in range(L):
+        for b in bound[l]:
+            b()
+    torch.cuda.synchronize()
+    n_eager = 6 * L
+    e0.record(st)
+    for i in range(n_eager):
+        for b in bound[i % L]:
+            b()
+    e1.record(st)
+    torch.cuda.synchronize()
+    eager_us = e0.elapsed_time(e1) * 1e3 / n_eager
+    log(f"decode layer (eager, pre-bound C-ABI calls): {eager_us:.2f} us/step")
+    del g_layers, g_rem
 
     # ---------------------------------------------------------------- per-kernel (graph, events)
+    # each projection rotates >= 512 MB of copies (layer copies plus extra ones)
     per_kernel = {}
     for p, (name, K, N) in enumerate(synth.LAYER):
-        g = capture(lambda i, p=p: ql.run(ws, layers[i % L][p], acts[p], out=outs[p], flags=flags[p]), L)
-        r = max(1, args.kernel_reps // L)
-        us = time_graph(g, r) * 1e6 / (r * L)
         b = N * K // 2 + N * 4
-        per_kernel[name] = {"us": round(us, 3), "bytes": b, "gbs": round(b / (us * 1e-6) / 1e9, 1)}
-        log(f"  gemv {name}: {us:.2f} us/launch, {per_kernel[name]['gbs']} GB/s")
+        n_copies = max(L, -(-ROTATE_BYTES // b))
+        pool = [layers[l][p] for l in range(L)]
+        for c in range(L, n_copies):
+            packed, codes, sc = synth.make_linear(N, K, 4, synth.linear_seed(c, p, workload=7), device=dev)
+            pool.append(ql.Weights.from_packed_device(4, K, N, packed, sc))
+            del packed, codes, sc
+        g = capture(lambda i, p=p, pool=pool: ql.run(ws, pool[i % len(pool)], acts[p], out=outs[p], flags=flags[p]),
+                    len(pool))
+        r = max(2, args.kernel_reps)
+        us = time_graph(g, r) * 1e6 / (r * len(pool))
+        per_kernel[name] = {"us": round(us, 3), "bytes": b, "gbs": round(b / (us * 1e-6) / 1e9, 1),
+                            "copies_rotated": len(pool), "rotated_bytes": b * len(pool)}
+        log(f"  gemv {name}: {us:.2f} us/launch, {per_kernel[name]['gbs']} GB/s ({len(pool)} copies)")
         del g
+        for w in pool[L:]:
+            w.close()
     dom = per_kernel["gate_up"]
 
-    # ---------------------------------------------------------------- prefill GEMM M=512
-    M = 512
-    pre_acts = [synth.activations(M, K, seed=synth.linear_seed(0, p) + 2, device=dev)
-                for p, (_, K, _) in enumerate(synth.LAYER)]
-    pre_outs = [torch.empty((M, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
-                for name, K, N in synth.LAYER]
+    # ---------------------------------------------------------------- W8 GEMV, M=1, K=N=2560
+    K1 = N1 = 2560
+    b1 = N1 * K1 + N1 * 4
+    n1 = -(-ROTATE_BYTES // b1)
+    w8 = []
+    for c in range(n1):
+        packed, codes, sc = synth.make_linear(N1, K1, 8, synth.linear_seed(c, 0, workload=1), device=dev)
+        w8.append(ql.Weights.from_packed_device(8, K1, N1, packed, sc))
+        del packed, codes, sc
+    x1 = synth.activations(1, K1, seed=synth.linear_seed(0, 0, workload=1) + 1, device=dev)
+    y1 = torch.empty((1, N1), dtype=torch.float16, device=dev)
+    g = capture(lambda i: ql.run(ws, w8[i % n1], x1, out=y1), n1)
+    r = max(2, args.kernel_reps)
+    us = time_graph(g, r) * 1e6 / (r * n1)
+    w8_line = {"workload": "W8A8 GEMV M=1 K=N=2560, int8 codes U[-127,127], scales U(0.002,0.02)",
+               "us": round(us, 3), "bytes": b1, "gbs": round(b1 / (us * 1e-6) / 1e9, 1),
+               "frac_of_hbm": round(b1 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies_rotated": n1}
+    log(f"  W8 GEMV 2560x2560 M=1: {us:.2f} us/launch, {w8_line['gbs']} GB/s ({n1} copies)")
+    del g
+    for w in w8:
+        w.close()
+
+    # ---------------------------------------------------------------- prefill M=512
     prefill = {}
-    tot_ops, tot_us = 0.0, 0.0
+    tot_ops, tot_us, tot_gemm_us = 0.0, 0.0, 0.0
     for p, (name, K, N) in enumerate(synth.LAYER):
         g = capture(lambda i, p=p: ql.run(ws, layers[i % L][p], pre_acts[p], out=pre_outs[p], flags=flags[p]), L)
         r = max(1, args.prefill_reps)
         us = time_graph(g, r) * 1e6 / (r * L)
-        ops = 2.0 * M * N * K
+        del g
+        g = capture(lambda i, p=p: gemm_only(p, i), L)
+        us_g = time_graph(g, r) * 1e6 / (r * L)
+        del g
+        ops = 2.0 * M512 * N * K
         tot_ops += ops
         tot_us += us
-        prefill[name] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1)}
-        log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM)")
-        del g
+        tot_gemm_us += us_g
+        prefill[name] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                         "gemm_us": round(us_g, 2), "gemm_tops": round(ops / (us_g * 1e-6) / 1e12, 1)}
+        log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM); "
+            f"GEMM alone {us_g:.1f} us, {prefill[name]['gemm_tops']} TOPS")
     prefill_tops = tot_ops / (tot_us * 1e-6) / 1e12
+    dom_p = max(prefill, key=lambda n: prefill[n]["gemm_us"])
+    dom_ops = 2.0 * M512 * dict((n, (K, N)) for n, K, N in synth.LAYER)[dom_p][0] * \
+        dict((n, (K, N)) for n, K, N in synth.LAYER)[dom_p][1]
+    roofline_m512 = {
+        "bound": "mfma", "kernel": f"GEMM {dom_p} M=512 (quantized rows in, fp16 out)",
+        "achieved": prefill[dom_p]["gemm_tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+        "frac": round(prefill[dom_p]["gemm_tops"] / INT8_PEAK_TOPS, 4), "ops_per_launch": dom_ops,
+        "us_per_launch": prefill[dom_p]["gemm_us"],
+    }
 
     # ---------------------------------------------------------------- W8 lm_head at M=1
     # 151,936 x 2560 int8 (389 MB, larger than the Infinity Cache): one GEMV launch.
@@ -253,7 +366,7 @@ def main():
     stack = None
     if L >= 1 and not args.no_stack:
         t0 = time.time()
-        w8 = []
+        w8s = []
         for l in range(L):
             pair = []
             for p in (1, 3):
@@ -262,7 +375,7 @@ def main():
                                                       stack=True)
                 pair.append(ql.Weights.from_packed_device(8, K, N, packed, sc))
                 del packed, codes, sc
-            w8.append(pair)
+            w8s.append(pair)
         gam = [(synth.gamma(synth.HIDDEN, seed=40000 + 2 * l, device=dev),
                 synth.gamma(synth.HIDDEN, seed=40001 + 2 * l, device=dev)) for l in range(L)]
         torch.cuda.synchronize()
@@ -275,18 +388,16 @@ def main():
             x = synth.activations(M, synth.HIDDEN, seed=40100 + M, device=dev)
             mids = [torch.empty((M, N // 2 if n == "gate_up" else N), dtype=torch.float16, device=dev)
                     for n, K, N in synth.LAYER]
-            hs = [torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev) for _ in range(2)]
-
-            hs.append(torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev))
+            hs = [torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev) for _ in range(3)]
 
             def stack_step(_i, M=M, x=x, mids=mids, hs=hs):
                 h = x
                 for l in range(L):
                     h1, h2 = hs[(2 * l) % 3], hs[(2 * l + 1) % 3]
                     ql.run(ws, layers[l][0], h, out=mids[0], gamma=gam[l][0], eps=1e-6)
-                    ql.run(ws, w8[l][0], mids[0][:, :4096], out=h1, residual=h)
+                    ql.run(ws, w8s[l][0], mids[0][:, :4096], out=h1, residual=h)
                     ql.run(ws, layers[l][2], h1, out=mids[2], flags=ql.QLIN_SWIGLU, gamma=gam[l][1], eps=1e-6)
-                    ql.run(ws, w8[l][1], mids[2], out=h2, residual=h1)
+                    ql.run(ws, w8s[l][1], mids[2], out=h2, residual=h1)
                     h = h2
 
             g = capture(stack_step, 1)
@@ -298,9 +409,9 @@ def main():
                 b = 4 * l
                 hid = b - 1 if l else -1
                 stages += [dict(weights=layers[l][0], gamma=gam[l][0], eps=1e-6, input=hid),
-                           dict(weights=w8[l][0], input=b, offset=0, residual=hid),
+                           dict(weights=w8s[l][0], input=b, offset=0, residual=hid),
                            dict(weights=layers[l][2], flags=ql.QLIN_SWIGLU, gamma=gam[l][1], eps=1e-6, input=b + 1),
-                           dict(weights=w8[l][1], input=b + 2, residual=b + 1)]
+                           dict(weights=w8s[l][1], input=b + 2, residual=b + 1)]
             chain = ql.Chain(stages, max_rows=M)
             yc = torch.empty((M, synth.HIDDEN), dtype=torch.float16, device=dev)
             g = capture(lambda _i: chain.run(x, out=yc), 1)
@@ -318,6 +429,9 @@ def main():
             }
             log(f"  stack {L} layers M={M}: launches {us_l:.0f} us ({stack[f'm{M}']['launches_gbs']} GB/s), "
                 f"chain {us_c:.0f} us ({stack[f'm{M}']['chain_gbs']} GB/s), outputs equal: {same and ok}")
+        for pair in w8s:
+            for w in pair:
+                w.close()
 
     # ---------------------------------------------------------------- prefill M=4096, fused RMSNorm
     long_prefill = None
@@ -354,7 +468,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         from oracle import oracle as orc
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        nproc = len(os.sched_getaffinity(0))
+        threads = nproc
         a_host = [a.cpu().numpy().view(np.uint16) for a in acts]
         n_layers, t0 = 0, time.perf_counter()
         while True:
@@ -367,9 +482,11 @@ def main():
                 break
         cpu_gbs = bytes_layer * n_layers / el / 1e9
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "nproc": nproc, "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
                "sample": f"{n_layers} passes of the same M=1 W4 layer (4 linears, fp16 in/out) in "
-                         f"{el:.1f} s with the C oracle (OpenMP, int8 codes unpacked in host memory)"}
-        log(f"cpu baseline: {cpu_gbs:.2f} GB/s on {threads} threads")
+                         f"{el:.1f} s with the C oracle (OpenMP on all {nproc} host cores available to the "
+                         f"process, int8 codes unpacked in host memory)"}
+        log(f"cpu baseline: {cpu_gbs:.2f} GB/s on {threads} threads (nproc {nproc})")
 
     result = {
         "metric": "weight-stream GB/s @M=1 + int8 TOPS @M=512, Qwen3-4B W4A8 linears",
@@ -379,6 +496,7 @@ def main():
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "step_time_distribution": dist,
         "eager_us_per_step": round(eager_us, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -402,9 +520,12 @@ def main():
             "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(),
         },
+        "roofline_m512": roofline_m512,
         "cpu_baseline": cpu,
         "per_kernel_decode": per_kernel,
+        "w8_gemv_2560": w8_line,
         "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
+                         "gemm_only_tops": round(tot_ops / (tot_gemm_us * 1e-6) / 1e12, 1),
                          "per_proj": prefill},
         "lm_head_w8_m1": head,
         "decode_stack_mixed": stack,

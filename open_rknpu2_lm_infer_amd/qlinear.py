@@ -170,6 +170,25 @@ class Chain:
             pass
 
 
+class BoundRun:
+    """One qlin_run call with every argument bound once (handles, device pointers, strides,
+    stream): calling it makes a single C-ABI call, the way a native engine's decode loop calls
+    the library, so eager launch timings measure the library rather than Python."""
+
+    def __init__(self, ws: Workspace, w: Weights, A: torch.Tensor, out: torch.Tensor, flags: int = 0,
+                 stream: torch.cuda.Stream | None = None):
+        assert A.stride(1) == 1 and out.stride(1) == 1
+        self._fn = _lib.load().qlin_run
+        st = (stream or torch.cuda.current_stream()).cuda_stream
+        self._args = (ws.handle, w.handle, A.shape[0], A.data_ptr(), _DT[A.dtype], A.stride(0), out.data_ptr(),
+                      _DT[out.dtype], out.stride(0), flags, st)
+
+    def __call__(self) -> None:
+        rc = self._fn(*self._args)
+        if rc:
+            check(rc, "qlin_run")
+
+
 def tune(ws: Workspace, w: Weights, rows: int, flags: int = 0, reps: int = 20) -> None:
     """Time the kernel variants of (w, rows, flags) and record the fastest (qlin_tune)."""
     check(_lib.load().qlin_tune(ws.handle, w.handle, rows, flags, reps, _stream()), "qlin_tune")
