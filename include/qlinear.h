@@ -308,7 +308,9 @@ typedef struct qlin_chain_stage {
 
 /* Checks the stages (K of each stage = the columns it reads; K % 8 == 0) and
  * allocates the intermediate fp16 buffers for max_rows <= 4 rows.  The weights must
- * outlive the chain. */
+ * outlive the chain.  Each CU's share of a stage must fit its registers at once: at
+ * most 80 steps of 128 weight bytes per CU (W8 K=9728 on N=2560 takes 76 on 256 CUs);
+ * larger stages return QLIN_ERR_UNSUPPORTED (run them with qlin_run). */
 int qlin_chain_create(const qlin_chain_stage* stages, int32_t n_stages, int32_t max_rows,
                       qlin_chain** out);
 void qlin_chain_free(qlin_chain* chain);
@@ -318,10 +320,11 @@ void qlin_chain_free(qlin_chain* chain);
 int qlin_chain_run(qlin_chain* chain, int32_t rows, const void* x, int64_t ldx, void* y, int64_t ldy,
                    void* stream);
 
-/* Polls of a stage counter (each followed by a short sleep) before a workgroup gives up
- * waiting and sets the QLIN_ERR_DEVICE bit of the chain's error word.  Default 4194304
- * (~0.2 s; QLIN_CHAIN_SPIN_LIMIT at chain creation overrides it); 0 gives up at once,
- * which tests use to exercise the failure path without any kernel hanging. */
+/* Polls of the previous stage's completion flags (each followed by a short sleep)
+ * before a workgroup gives up waiting and sets the QLIN_ERR_DEVICE bit of the chain's
+ * error word.  Default 262144 (~0.3 s; QLIN_CHAIN_SPIN_LIMIT at chain creation overrides
+ * it); 0 gives up at once, which tests use to exercise the failure path without any
+ * kernel hanging. */
 int qlin_chain_set_wait_limit(qlin_chain* chain, int32_t polls);
 
 /* Device pointer and row stride (elements) of stage `stage`'s fp16 output from the
@@ -330,10 +333,9 @@ int qlin_chain_stage_output(const qlin_chain* chain, int32_t stage, void** ptr, 
 
 /* Error word of the runs since the last clear: QLIN_OK, QLIN_ERR_NONFINITE (an input
  * row held Inf/NaN) or QLIN_ERR_DEVICE (a stage wait gave up: the grid was not fully
- * resident, e.g. other work occupied the GPU; the outputs are then invalid).
- * Synchronizes the last run's stream.  clear != 0 resets the word.  After a run that
- * gave up, the stage counters may be left mid-count: call qlin_chain_status (which
- * restarts them from zero) before the chain runs again. */
+ * resident, e.g. other work occupied the GPU; that run's outputs are invalid).
+ * Synchronizes the last run's stream.  clear != 0 resets the word.  A run that gave up
+ * leaves no state behind: the next run is correct without any reset. */
 int qlin_chain_status(qlin_chain* chain, int32_t clear);
 
 #ifdef __cplusplus

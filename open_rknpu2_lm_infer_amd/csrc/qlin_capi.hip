@@ -1029,14 +1029,16 @@ struct qlin_chain {
     int n, max_rows, device, grid;
     int x_cols;        // chain-input columns read by the stages
     int last_cols;     // output columns of the last stage
-    int kp_max, k_max;
-    size_t lds, q_bytes, red_bytes;
+    int kp_max, k_max, kg_max, ipw_max;
+    size_t lds;
+    ChainParams layout;              // LDS carve-up
     std::vector<ChainStage> stages;  // host copy
     std::vector<int> cols;           // output columns per stage
     ChainStage* d_stages;
     std::vector<_Float16*> outs;     // per stage, null for the last
     std::vector<int64_t> ld;
-    uint32_t* counters;
+    uint32_t* flags;   // [n][kChainFlagStride] completion epochs
+    uint32_t* epochs;  // [grid] launches per workgroup
     uint32_t* err;
     int spin_limit;  // polls per stage wait before the kernel gives up (QLIN_CHAIN_SPIN_LIMIT)
     hipStream_t last;
@@ -1047,9 +1049,18 @@ void qlin_chain_free(qlin_chain* c) {
     if (c->last) (void)hipStreamSynchronize(c->last);
     for (auto* o : c->outs) (void)hipFree(o);
     (void)hipFree(c->d_stages);
-    (void)hipFree(c->counters);
+    (void)hipFree(c->flags);
+    (void)hipFree(c->epochs);
     (void)hipFree(c->err);
     delete c;
+}
+
+// Items of a stage: each of the grid's workgroups owns ipw items of iw <= 16 output
+// channels, the fewest channels per workgroup that cover the stage.
+static void chain_items(int cols, int grid, int* iw, int* ipw) {
+    const int per = (cols + grid - 1) / grid;
+    *ipw = (per + 15) / 16;
+    *iw = (per + *ipw - 1) / *ipw;
 }
 
 int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, qlin_chain** out) {
@@ -1063,13 +1074,14 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
     c->n = n;
     c->max_rows = max_rows;
     c->device = dev;
-    c->spin_limit = env_int("QLIN_CHAIN_SPIN_LIMIT", 1 << 22);  // ~0.2 s of polling per wait
+    c->grid = cu_count(dev);
+    c->spin_limit = env_int("QLIN_CHAIN_SPIN_LIMIT", 1 << 18);  // ~0.3 s of polling per wait
     c->stages.resize(n);
     c->cols.resize(n);
     c->outs.assign(n, nullptr);
     c->ld.assign(n, 0);
     const uint32_t allowed = QLIN_SWIGLU | QLIN_ROUND_HALF_EVEN | QLIN_NORM_SEQUENTIAL | QLIN_RESIDUAL;
-    int rc = QLIN_OK;
+    int rc = c->grid > 0 && c->grid <= kChainFlagStride ? QLIN_OK : QLIN_ERR_UNSUPPORTED;
     for (int s = 0; s < n && rc == QLIN_OK; ++s) {
         const qlin_chain_stage& d = st[s];
         const qlin_weights* w = d.weights;
@@ -1078,7 +1090,11 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
             rc = QLIN_ERR_PARAM;
             break;
         }
-        if ((d.flags & QLIN_SWIGLU) && w->N % 64) {
+        if ((d.flags & QLIN_SWIGLU) && w->N % 2) {
+            rc = QLIN_ERR_PARAM;
+            break;
+        }
+        if ((int64_t)w->Np * w->wrow >= ((int64_t)1 << 31)) {  // 32-bit buffer offsets
             rc = QLIN_ERR_UNSUPPORTED;
             break;
         }
@@ -1112,24 +1128,33 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
         cs.N = w->N;
         cs.Np = w->Np;
         cs.flags = (int)(d.flags & (kFlagSwiglu | kFlagRne | kFlagNormSeq));
-        cs.groups = ((d.flags & QLIN_SWIGLU) ? w->N / 2 : w->Np) / 16;
+        cs.ncols = c->cols[s];
+        chain_items(cs.ncols, c->grid, &cs.iw, &cs.ipw);
+        cs.steps = w->Kp / (w->bits == 4 ? 256 : 128);
+        // a workgroup's share of the stage must fit the compute waves' registers at once
+        if (((d.flags & QLIN_SWIGLU) ? 2 : 1) * cs.ipw * cs.steps > chain_round_capacity()) {
+            rc = QLIN_ERR_UNSUPPORTED;
+            break;
+        }
         cs.gamma = d.gamma;
         cs.eps = d.eps;
         cs.x_offset = d.input == -1 ? d.input_offset : 0;
         cs.res_kind = (d.flags & QLIN_RESIDUAL) ? (d.residual == -1 ? 1 : 2) : 0;
+        cs.res_stage = cs.res_kind == 2 ? d.residual : -1;
         cs.res_x_offset = cs.res_kind == 1 ? d.residual_offset : 0;
         cs.rmult = d.residual_multiplier;
         c->kp_max = std::max(c->kp_max, w->Kp);
         c->k_max = std::max(c->k_max, w->K);
+        if (d.gamma) c->kg_max = std::max(c->kg_max, w->K);
+        c->ipw_max = std::max(c->ipw_max, cs.ipw);
     }
     if (rc == QLIN_OK) {
         c->last_cols = c->cols[n - 1];
-        c->lds = chain_lds_bytes(max_rows, c->kp_max, c->k_max, &c->q_bytes, &c->red_bytes);
+        c->lds = chain_lds_layout(max_rows, c->kp_max, c->k_max, c->kg_max, c->ipw_max, &c->layout);
         if (c->lds > (size_t)kChainMaxLds) rc = QLIN_ERR_UNSUPPORTED;
     }
     // one workgroup per CU; every workgroup must be resident for the stage waits
     if (rc == QLIN_OK && chain_resident_per_cu(max_rows, c->lds) < 1) rc = QLIN_ERR_UNSUPPORTED;
-    c->grid = cu_count(dev);
     for (int s = 0; s < n - 1 && rc == QLIN_OK; ++s) {
         c->ld[s] = round_up(c->cols[s], 8);
         if (hipMalloc(&c->outs[s], (size_t)max_rows * c->ld[s] * sizeof(_Float16)) != hipSuccess) rc = QLIN_ERR_NOMEM;
@@ -1146,14 +1171,16 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
             cs.ld_res = c->ld[st[s].residual];
         }
     }
+    const size_t flag_bytes = sizeof(uint32_t) * (size_t)n * kChainFlagStride;
     if (rc == QLIN_OK &&
-        (hipMalloc(&c->d_stages, sizeof(ChainStage) * n) != hipSuccess ||
-         hipMalloc(&c->counters, sizeof(uint32_t) * n) != hipSuccess || hipMalloc(&c->err, sizeof(uint32_t)) != hipSuccess))
+        (hipMalloc(&c->d_stages, sizeof(ChainStage) * n) != hipSuccess || hipMalloc(&c->flags, flag_bytes) != hipSuccess ||
+         hipMalloc(&c->epochs, sizeof(uint32_t) * c->grid) != hipSuccess || hipMalloc(&c->err, sizeof(uint32_t)) != hipSuccess))
         rc = QLIN_ERR_NOMEM;
     if (rc == QLIN_OK &&
         (hipMemcpy(c->d_stages, c->stages.data(), sizeof(ChainStage) * n, hipMemcpyHostToDevice) != hipSuccess ||
-         hipMemset(c->counters, 0, sizeof(uint32_t) * n) != hipSuccess || hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess ||
-         hipDeviceSynchronize() != hipSuccess))
+         hipMemset(c->flags, 0, flag_bytes) != hipSuccess ||
+         hipMemset(c->epochs, 0, sizeof(uint32_t) * c->grid) != hipSuccess ||
+         hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess))
         rc = QLIN_ERR_DEVICE;
     if (rc != QLIN_OK) {
         qlin_chain_free(c);
@@ -1170,7 +1197,7 @@ int qlin_chain_run(qlin_chain* c, int32_t rows, const void* x, int64_t ldx, void
     int dev;
     if (int rc = current_device(&dev)) return rc;
     if (dev != c->device) return QLIN_ERR_PARAM;
-    ChainParams p{};
+    ChainParams p = c->layout;
     p.stages = c->d_stages;
     p.n_stages = c->n;
     p.M = rows;
@@ -1178,12 +1205,11 @@ int qlin_chain_run(qlin_chain* c, int32_t rows, const void* x, int64_t ldx, void
     p.ldx = ldx;
     p.y = reinterpret_cast<_Float16*>(y);
     p.ldy = ldy;
-    p.counters = c->counters;
+    p.flags = c->flags;
+    p.epochs = c->epochs;
     p.err = c->err;
     p.spin_limit = c->spin_limit;
     p.kp_max = c->kp_max;
-    p.lds_q_bytes = (int)c->q_bytes;
-    p.lds_red_bytes = (int)c->red_bytes;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     c->last = st;
     return launch_chain(p, c->grid, c->lds, st) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
@@ -1207,10 +1233,8 @@ int qlin_chain_status(qlin_chain* c, int32_t clear) {
     if (hipStreamSynchronize(c->last) != hipSuccess) return QLIN_ERR_DEVICE;
     uint32_t e = 0;
     if (hipMemcpy(&e, c->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return QLIN_ERR_DEVICE;
-    if (e & 2u) {
-        // a wait gave up: the counters may be left mid-count; restart them from zero
-        if (hipMemset(c->counters, 0, sizeof(uint32_t) * c->n) != hipSuccess) return QLIN_ERR_DEVICE;
-    }
+    // a wait that gave up leaves nothing to repair: every workgroup still ran the launch
+    // to its end and counted its epoch, so the next launch's flags are all fresh
     if (clear && e && hipMemset(c->err, 0, sizeof(uint32_t)) != hipSuccess) return QLIN_ERR_DEVICE;
     if (hipDeviceSynchronize() != hipSuccess) return QLIN_ERR_DEVICE;
     return (e & 2u) ? QLIN_ERR_DEVICE : (e ? QLIN_ERR_NONFINITE : QLIN_OK);

@@ -1,421 +1,697 @@
 // Decode chain: a sequence of quantized linears in one persistent launch (a decoder
 // layer's projections, or a stack of layers), for 1..4 rows.  Each stage is the
-// decode GEMV of one weight matrix (kernel (b) + (d)) with its activation quantization
-// (kernel (a), after an optional RMSNorm) fused into the prologue, exactly as the
-// single-linear entry points compute it.  Replaces the engine's per-linear calls of
-// the decode step (src/model/dense.rs:470-530 driving src/npu.rs Linear::run).
+// decode GEMV of one weight matrix (kernels (b) + (d)) with its activation
+// quantization (kernel (a), after an optional RMSNorm) and optional residual update,
+// exactly as the single-linear entry points compute it.  Replaces the engine's
+// per-linear calls of the decode step (src/model/dense.rs:398-540 driving
+// src/npu.rs Linear::run).
 //
-// Grid.  One 512-thread workgroup per CU (all resident at once).  Stage s has
-// groups_s items of 16 output channels over the whole K; workgroup b owns items
-// b, b + G, b + 2G, ... and processes them in rounds of up to four, its 8 waves split
-// evenly over the round's items and each item's waves splitting the K steps.
+// Grid.  One workgroup per CU, all resident at once.  Each workgroup owns a fixed,
+// contiguous range of output channels of every stage: ipw items of iw channels, sized
+// on the host so the grid covers the stage's channels with the fewest channels per
+// workgroup (e.g. 10 of N = 2560 on 256 CUs).  An item is one 16-row MFMA tile over
+// the whole K; rows past the item's width re-read its last row and are not stored.
 //
-// Dependencies.  An item's weights do not depend on activations, so each wave issues
-// its first batch of weight loads for a round before waiting for the previous stage:
-// the weight stream keeps running while the stage boundary resolves.  A stage's
-// outputs are written with device-coherent stores; after its last item a workgroup
-// waits for its stores and adds its item count to the stage's counter.  The first
-// round of the next stage waits (thread 0, bounded spin) until that counter reaches
-// the stage's item count, then every workgroup loads the rows with device-coherent
-// loads, applies the RMSNorm if configured, and quantizes them into LDS.  The
-// workgroup completing the last stage resets the counters for the next launch.  A
-// wait that exceeds the spin bound sets bit 1 of the error word and gives up, so every
-// wave always reaches the end of the kernel.
-#include <type_traits>
-
+// Waves.  Four compute waves (one per SIMD) and four helper waves.  The compute waves
+// hold their workgroup's share of a stage's weights in registers (up to 40 x 16 bytes
+// per lane) and issue no other global memory access, so the only thing they ever wait
+// for is their own weight loads.  The helper waves do everything else: the first one
+// (the I/O wave) polls the previous stage's completion flags, copies the stage input
+// rows and the RMSNorm weights into LDS with direct global -> LDS copies and reads the
+// per-channel scales and residual rows; all four compute the RMSNorm, per-token scale
+// and quantized rows into LDS; after the products the I/O wave runs the epilogue and
+// stores this workgroup's outputs.  The two groups never share a barrier: the compute
+// waves wait for LDS words (input rows landed, quantized rows ready) and count
+// themselves done in another; the helpers synchronize among themselves with an LDS
+// counter.
+//
+// Per stage: (I/O) wait for stage s - 1, rows -> LDS | (compute) issue the stage's
+// weight loads | (helpers) RMSNorm, per-token scale and quantized rows into LDS, same
+// arithmetic as the GEMV prologue, then "rows ready" | (compute) MFMA over the weights
+// in registers, int32 sums added into LDS, "done" | (I/O) dequant / SiLU-gate /
+// residual epilogue, fp16 stores, then this workgroup's flag for stage s.  The weight
+// loads start only once the input rows have landed: loads in flight during the
+// exchange sit ahead of its polls, copies and stores in the CU's memory pipeline and
+// delay every stage more than they save.
+//
+// Completion flags.  flags[s][b] holds the launch epoch in which workgroup b finished
+// its part of stage s.  Workgroup b counts its launches in epochs[b]; all workgroups
+// run every launch to its end, so they agree on the epoch and no flag or counter is
+// ever reset (a graph replay is just the next epoch).  Outputs are written with
+// device-coherent stores; the I/O wave waits for their completion before it stores the
+// flag, and reads stage inputs with device-coherent loads after seeing every flag of
+// the stage.  Every stage waits for the whole previous stage, so every earlier stage is
+// complete as well.  A wait that exceeds the spin bound sets bit 1 of the error word
+// and gives up, so every wave always reaches the end of the kernel.
 #include "qlin_chain.hpp"
 #include "qlin_gemv_parts.hpp"
 #include "qlin_rows.hpp"
 
 namespace qlin {
 
-constexpr int kChainWaves = 8;
-constexpr int kChainThreads = 64 * kChainWaves;
-static_assert(kChainThreads == kChainThreadsPerBlock, "host and kernel agree on the block size");
-constexpr int kChainBatch = 2;  // wave steps per register buffer
+constexpr int kCW = kChainComputeWaves;
+constexpr int kHW = kChainHelperWaves;
+constexpr int kHT = 64 * kHW;  // helper threads
+constexpr int kCT = kChainThreadsPerBlock;
+constexpr int kNB = kChainBufRegs;
+constexpr int kSc1 = 16;  // cache policy: coherent at device scope
+constexpr int kRsrcFlags = 0x00020000;
 
 typedef unsigned int u32x4c __attribute__((ext_vector_type(4)));
-constexpr int kChainRsrc = 0x00020000;
-constexpr int kSc1 = 16;  // cache policy: coherent at device scope
+typedef __attribute__((address_space(3))) void* chain_lds_ptr;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t chain_rsrc(const void* base, int64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kChainRsrc);
+constexpr int kCMaxE = kNB / 2;  // weight steps a compute wave holds (two 16-byte loads each)
+
+
+// Wave index as a wave-uniform (scalar) value: offsets derived from it stay in SGPRs.
+__device__ __forceinline__ int c_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Stage descriptors are read through the constant address space: scalar loads, which
+// the compute waves can wait for without waiting for their weight loads.
+typedef __attribute__((address_space(4))) const ChainStage ChainStageConst;
+__device__ __forceinline__ ChainStage c_desc(const ChainParams& p, int s) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return ((ChainStageConst*)p.stages)[s];
+#else
+    return p.stages[s];  // the host pass never runs device code
+#endif
 }
 
-// Registers of one batch of wave steps: gate (or plain) and up weight blocks.
-template <bool SWIGLU>
-struct ChainBuf {
-    v4i bg[kChainBatch][2];
-    v4i bu[SWIGLU ? kChainBatch : 1][2];
+int chain_round_capacity() { return kCW * kCMaxE; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t c_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
+}
+
+// Items of stage st owned by workgroup b; item i covers output channels
+// [c_first, c_first + c_width).
+__device__ __forceinline__ int c_items(const ChainStage& st, int b) {
+    const int c0 = b * st.ipw * st.iw;
+    if (c0 >= st.ncols) return 0;
+    const int n = (st.ncols - c0 + st.iw - 1) / st.iw;
+    return n < st.ipw ? n : st.ipw;
+}
+__device__ __forceinline__ int c_first(const ChainStage& st, int b, int i) { return (b * st.ipw + i) * st.iw; }
+__device__ __forceinline__ int c_width(const ChainStage& st, int b, int i) {
+    const int w = st.ncols - c_first(st, b, i);
+    return w < st.iw ? w : st.iw;
+}
+
+// Row items: with SwiGLU each channel item contributes a gate item (rows c) and an up
+// item (rows N/2 + c), interleaved, so every stage streams plain 16-row items.
+__device__ __forceinline__ int c_row_items(const ChainStage& st, int n_it) {
+    return (st.flags & kFlagSwiglu) ? 2 * n_it : n_it;
+}
+
+// Weight steps f0 .. f0 + cnt - 1 of the workgroup's flat (row item, step) sequence
+// into buf: lane (r, g) = (lane & 15, lane >> 4) loads bytes 16g and 64 + 16g of the
+// 128-byte step of row r.  Every slot is loaded: slots past cnt read past the end of
+// the buffer resource, which returns zeros without a memory access, so buf is written
+// whole on one code path.
+template <int E0, int E1>
+__device__ __forceinline__ void c_load(v4i (&buf)[kNB], const ChainStage& st, int b, int f0, int cnt) {
+    const int lane = threadIdx.x & 63;
+    const bool sw = (st.flags & kFlagSwiglu) != 0;
+    const __amdgpu_buffer_rsrc_t r = c_rsrc(st.W, (int64_t)st.Np * st.wrow);
+    const int wrow = (int)st.wrow, up_off = (st.N >> 1) * wrow, lo = (lane >> 4) * 16;
+    int ri = (f0 + E0) / st.steps, t = (f0 + E0) - ri * st.steps;
+    int off = 0;
+#pragma unroll
+    for (int e = E0; e < E1; ++e) {
+        if (e == E0 || t == 0) {  // row offset of a new row item (one VALU multiply)
+            const int i = sw ? ri >> 1 : ri;
+            const int row = c_first(st, b, i) + min(lane & 15, c_width(st, b, i) - 1);
+            off = row * wrow + lo + ((sw && (ri & 1)) ? up_off : 0);
+        }
+        const int o = e < cnt ? off : (int)0x80000000;  // past the resource: zeros, no access
+        buf[2 * e] = __builtin_amdgcn_raw_buffer_load_b128(r, o, t * 128, 0);
+        buf[2 * e + 1] = __builtin_amdgcn_raw_buffer_load_b128(r, o, t * 128 + 64, 0);
+        if (++t == st.steps) {
+            t = 0;
+            ++ri;
+        }
+    }
+}
+
+// Weight steps E0 .. E1 - 1 of this wave's share of stage s.
+template <int E0, int E1>
+__device__ __forceinline__ void c_load_stage(const ChainParams& p, int s, v4i (&buf)[kNB]) {
+    const ChainStage st = c_desc(p, s);
+    const int wave = c_wave(), b = blockIdx.x;
+    const int E = c_row_items(st, c_items(st, b)) * st.steps;
+    const int f0 = E * wave / kCW, f1 = E * (wave + 1) / kCW;
+    c_load<E0, E1>(buf, st, b, f0, f1 - f0);
+}
+
+// Sums of one row item into LDS: lanes 0..15 hold channel `lane`, rows 0..3 in acc[0..3].
+template <int MR>
+__device__ __forceinline__ void c_flush(const ChainStage& st, int b, int ri, const v4i& acc, int M, int* accg,
+                                        int* accu) {
+    const int lane = threadIdx.x & 63;
+    const bool sw = (st.flags & kFlagSwiglu) != 0;
+    const int i = sw ? ri >> 1 : ri;
+    int* dst = (sw && (ri & 1)) ? accu : accg;
+    if (lane < c_width(st, b, i)) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+            if (r < M) atomicAdd(dst + (i * 16 + lane) * MR + r, acc[r]);
+    }
+}
+
+// Matrix products of weight steps f0 .. f0 + cnt - 1 (already in buf) with the
+// quantized rows in LDS.  One code path for both widths (a uniform branch per step),
+// so the weight registers have a single consumer in the compute waves' loop.
+template <int MR>
+__device__ __forceinline__ void c_compute(const v4i (&buf)[kNB], const ChainStage& st, int b, int f0, int cnt,
+                                          const uint8_t* lds_q, int astride, int M, int* accg, int* accu) {
+    const bool w4 = st.bits == 4;
+    const int KS = w4 ? 256 : 128;
+    const int lane = threadIdx.x & 63, ml = lane & 15;
+    const uint8_t* arow = lds_q + (ml < M ? ml : M) * astride + (lane >> 4) * (w4 ? 32 : 16);
+    int ri = f0 / st.steps, t = f0 - ri * st.steps;
+    v4i acc = {0, 0, 0, 0};
+    bool pending = false;
+#pragma unroll
+    for (int e = 0; e < kCMaxE; ++e) {
+        if (e < cnt) {
+            const v4i w[2] = {buf[2 * e], buf[2 * e + 1]};
+            v4i a[4];
+            if (w4) {
+                a_from_lds<4>(a, arow + t * KS);
+                mfma_step<4>(acc, w, a);
+            } else {
+                a_from_lds<8>(a, arow + t * KS);
+                mfma_step<8>(acc, w, a);
+            }
+            pending = true;
+            if (++t == st.steps) {
+                c_flush<MR>(st, b, ri, acc, M, accg, accu);
+                acc = v4i{0, 0, 0, 0};
+                pending = false;
+                t = 0;
+                ++ri;
+            }
+            // one step at a time: hoisting later steps' operand reads would need
+            // registers the weight buffer holds
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (pending) c_flush<MR>(st, b, ri, acc, M, accg, accu);
+}
+
+// LDS words that order the waves of a workgroup (no s_barrier: the compute waves and
+// the helpers never wait at the same barrier).
+struct ChainSync {
+    uint32_t rows_ready;  // stages whose quantized rows are in LDS
+    uint32_t done;        // compute-wave completions, kCW per stage
+    uint32_t helpers;     // helper arrivals, kHW per helper barrier
+    uint32_t io_mark;     // 2s once stage s's input rows are in LDS (releases the compute
+                          // waves' weight loads of stage s)
 };
 
-// Unconditional loads: a step past the end re-reads the last one (an L2 hit).
-template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void chain_load(ChainBuf<SWIGLU>& b, const uint8_t* wg, const uint8_t* wu, int first,
-                                           int stride, int steps) {
-#pragma unroll
-    for (int i = 0; i < kChainBatch; ++i) {
-        const int st = min(first + stride * i, steps - 1);
-        b.bg[i][0] = ld16(wg + (int64_t)st * 128);
-        b.bg[i][1] = ld16(wg + (int64_t)st * 128 + 64);
-        if constexpr (SWIGLU) {
-            b.bu[i][0] = ld16(wu + (int64_t)st * 128);
-            b.bu[i][1] = ld16(wu + (int64_t)st * 128 + 64);
+__device__ __forceinline__ uint32_t lds_load(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Completes this wave's LDS accesses (not its global loads or stores).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Waits until *w >= target.
+__device__ __forceinline__ void lds_wait_ge(const uint32_t* w, uint32_t target) {
+    while (lds_load(w) < target) __builtin_amdgcn_s_sleep(1);
+}
+
+// Barrier of the kHW helper waves; k counts this wave's helper barriers.
+__device__ __forceinline__ void helper_sync(ChainSync* sy, uint32_t& k) {
+    wait_lds();  // this wave's LDS writes are visible before it arrives
+    ++k;
+    if ((threadIdx.x & 63) == 0) atomicAdd(&sy->helpers, 1u);
+    lds_wait_ge(&sy->helpers, kHW * k);
+}
+
+// Waits until every workgroup has finished its part of stage s (all flags == e).
+__device__ __forceinline__ void c_io_poll(const ChainParams& p, int s, uint32_t e) {
+    const int lane = threadIdx.x & 63, G = gridDim.x;
+    const __amdgpu_buffer_rsrc_t r = c_rsrc(p.flags + (int64_t)s * kChainFlagStride, kChainFlagStride * 4);
+    for (int spins = 0;; ++spins) {
+        bool ok = true;
+        for (int j0 = 0; j0 < G; j0 += 256) {
+            const int j = j0 + 4 * lane;
+            const u32x4c v = __builtin_amdgcn_raw_buffer_load_b128(r, j * 4, 0, kSc1);
+            ok &= (j >= G || v.x == e) && (j + 1 >= G || v.y == e) && (j + 2 >= G || v.z == e) &&
+                  (j + 3 >= G || v.w == e);
         }
+        if (__all(ok)) return;
+        if (spins >= p.spin_limit) {
+            if (lane == 0) atomicOr(p.err, 2u);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
     }
 }
 
-template <int BITS, bool SWIGLU>
-__device__ __forceinline__ void chain_compute(v4i& ag, v4i& au, const ChainBuf<SWIGLU>& b, const uint8_t* arow,
-                                              int first, int stride, int steps) {
-    constexpr int KS = BITS == 4 ? 256 : 128;
-#pragma unroll
-    for (int i = 0; i < kChainBatch; ++i) {
-        const int st = first + stride * i;
-        if (st < steps) {
-            v4i a[4];
-            a_from_lds<BITS>(a, arow + st * KS);
-            mfma_step<BITS>(ag, b.bg[i], a);
-            if constexpr (SWIGLU) mfma_step<BITS>(au, b.bu[i], a);
-        }
-    }
+__device__ __forceinline__ float c_residual(const ChainParams& p, const ChainStage& st, int m, int c) {
+    if (st.res_kind == 1) return __half2float(p.x[(int64_t)m * p.ldx + st.res_x_offset + c]);
+    const uint16_t bits = __hip_atomic_load(reinterpret_cast<const uint16_t*>(st.res) + (int64_t)m * st.ld_res + c,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (float)__builtin_bit_cast(_Float16, bits);
 }
 
-// Thread 0 waits until *cnt >= target (bounded), then the workgroup proceeds.
-__device__ __forceinline__ void chain_wait(const ChainParams& p, const uint32_t* cnt, uint32_t target) {
-    if (threadIdx.x == 0) {
-        int spins = 0;
-        while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++spins > p.spin_limit) {
-                atomicOr(p.err, 2u);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
+// I/O wave, before the stage: per-channel scales and residual rows of this workgroup's
+// outputs, the RMSNorm weights, the wait for stage s - 1, and the input rows.
+template <bool SW, int MR>
+__device__ __forceinline__ void c_io_input(const ChainParams& p, const ChainStage& st, int s, int b, int n_it,
+                                           uint32_t e, uint8_t* smem, ChainSync* sy) {
+    const int lane = threadIdx.x & 63, M = p.M;
+    const int nch = n_it * 16;
+    const int sc_up = p.ipw_max * 16;
+    float* lsc = reinterpret_cast<float*>(smem + p.off_sc);
+    float* lr = reinterpret_cast<float*>(smem + p.off_res);
+    // 1. scales and (when their source is already complete) residual rows
+    const bool small = nch <= 64;
+    const bool res_early = st.res_kind == 1 || st.res_stage <= s - 2;
+    const int ch = lane, ci = ch >> 4, cn = ch & 15;
+    const bool own = small && ch < nch && cn < c_width(st, b, ci);
+    const int cc = own ? c_first(st, b, ci) + cn : 0;
+    float scg = 0.0f, scu = 0.0f, rv[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) rv[m] = 0.0f;
+    if (own) {
+        scg = st.wscale[cc];
+        if constexpr (SW) scu = st.wscale[(st.N >> 1) + cc];
+        if (st.res_kind && res_early) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < M) rv[m] = c_residual(p, st, m, cc);
         }
     }
-    __syncthreads();
-}
-
-// Activation prologue of one stage: rows [0, M) of the stage input (fp16) into LDS,
-// RMSNorm scale, per-token scale, quantized rows in the order the stage's MFMA step
-// expects, a zero row M.  Same arithmetic as the GEMV's fused prologue.
-template <int BITS, int MR>
-__device__ void chain_prologue(const ChainParams& p, const ChainStage& st, const __half* in, int64_t ld_in,
-                               bool coherent, uint8_t* lds_q, int astride, __half* lds_x, float* s_rows,
-                               float* s_inv, float (*s_red)[4], int* s_bad) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int M = p.M, K = st.K;
-    const int ng = K >> 3;  // 8-value groups per row
-    // 1. raw rows into LDS, 16 bytes per load, all loads of a thread issued together
-    {
-        const __amdgpu_buffer_rsrc_t r = chain_rsrc(in, (int64_t)(M - 1) * ld_in * 2 + (int64_t)K * 2);
-        const int total = M * ng;
-        constexpr int B = 4;
-        for (int c0 = tid; c0 < total; c0 += kChainThreads * B) {
-            u32x4c v[B];
-#pragma unroll
-            for (int i = 0; i < B; ++i) {
-                const int c = min(c0 + kChainThreads * i, total - 1);
-                const int m = c / ng, g = c - m * ng;
-                const int off = (int)(((int64_t)m * ld_in + 8 * g) * 2);
-                v[i] = coherent ? __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1)
-                                : __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < B; ++i) {
-                const int c = min(c0 + kChainThreads * i, total - 1);
-                const int m = c / ng, g = c - m * ng;
-                *reinterpret_cast<u32x4c*>(lds_x + m * K + 8 * g) = v[i];
-            }
-        }
-    }
-    __syncthreads();
-    // 2. RMSNorm scale per row (wave m computes row m), reference summation order
+    // 2. RMSNorm weights: direct copies into LDS, 1 KiB per instruction
     if (st.gamma) {
-        if (wave < M) {
-            const __half* xr = lds_x + wave * K;
+        const __amdgpu_buffer_rsrc_t r = c_rsrc(st.gamma, (int64_t)st.K * 4);
+        const int chunks = (st.K * 4 + 1023) >> 10;
+        for (int c = 0; c < chunks; ++c)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (chain_lds_ptr)(smem + p.off_g + c * 1024), 16, c * 1024 + lane * 16,
+                                                     0, 0, 0);
+    }
+    // 3. wait for the previous stage
+    if (s > 0) c_io_poll(p, s - 1, e);
+    // 4. input rows: the chain input, or an earlier stage's output read device-coherently
+    {
+        const bool from_x = st.in == nullptr;
+        const __half* in = from_x ? p.x + st.x_offset : st.in;
+        const int64_t ld_in = from_x ? p.ldx : st.ld_in;
+        const int chunks = (st.K * 2 + 1023) >> 10;
+        for (int m = 0; m < M; ++m) {
+            const __amdgpu_buffer_rsrc_t r = c_rsrc(in + (int64_t)m * ld_in, (int64_t)st.K * 2);
+            uint8_t* dst = smem + p.off_x + m * p.xstride;
+            if (from_x) {
+                for (int c = 0; c < chunks; ++c)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (chain_lds_ptr)(dst + c * 1024), 16, c * 1024 + lane * 16, 0,
+                                                             0, 0);
+            } else {
+                for (int c = 0; c < chunks; ++c)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (chain_lds_ptr)(dst + c * 1024), 16, c * 1024 + lane * 16, 0,
+                                                             0, kSc1);
+            }
+        }
+    }
+    if (own && st.res_kind && !res_early) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < M) rv[m] = c_residual(p, st, m, cc);
+    }
+    if (small) {
+        if (ch < nch) {
+            lsc[ch] = scg;
+            if constexpr (SW) lsc[sc_up + ch] = scu;
+            if (st.res_kind) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) lr[ch * MR + m] = rv[m];
+            }
+        }
+    } else {
+        // wide stages (more than 64 channels per workgroup): one pass per 64 channels
+        for (int c2 = lane; c2 < nch; c2 += 64) {
+            const int i = c2 >> 4, n = c2 & 15;
+            if (n < c_width(st, b, i)) {
+                const int c = c_first(st, b, i) + n;
+                lsc[c2] = st.wscale[c];
+                if constexpr (SW) lsc[sc_up + c2] = st.wscale[(st.N >> 1) + c];
+                if (st.res_kind)
+                    for (int m = 0; m < M; ++m) lr[c2 * MR + m] = c_residual(p, st, m, c);
+            }
+        }
+    }
+    wait_all_memory();  // the direct copies into LDS have landed
+    if (lane == 0) __hip_atomic_store(&sy->io_mark, (uint32_t)(2 * s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Sum of squares of a row of K fp16 values in LDS, in the order of src/model/cpu.rs:14-35:
+// 16 fused-multiply-add chains (chain j takes elements j, j+16, ... in order), combined
+// lanewise as (a+b)+(c+d), then (t0+t1)+(t2+t3), then the scalar tail sum += v*v.  Lane j
+// of one wave runs chain j; the next eight elements' LDS reads are in flight while the
+// current eight FMAs run.  Result valid in lane 0.
+__device__ float c_sumsq_neon16(const __half* x, int K) {
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    float acc = 0.0f;
+    if (lane < 16) {
+        const int nb = (K & ~15) >> 7;  // batches of 8 elements per chain (128 per batch)
+        const int n8 = nb << 7;
+        float a[8], c[8];
+        if (nb > 0) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = __half2float(x[16 * u + j]);
+        }
+        for (int bt = 0; bt < nb; bt += 2) {
+            const int i = bt << 7;
+            if (bt + 1 < nb) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) c[u] = __half2float(x[i + 128 + 16 * u + j]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(a[u], a[u], acc);
+            if (bt + 1 >= nb) break;
+            if (bt + 2 < nb) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a[u] = __half2float(x[i + 256 + 16 * u + j]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(c[u], c[u], acc);
+        }
+        for (int i = n8; i < (K & ~15); i += 16) {  // the last partial batch
+            const float v = __half2float(x[i + j]);
+            acc = __builtin_fmaf(v, v, acc);
+        }
+    }
+    const float b = __shfl(acc, j + 4, 64), c2 = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
+    const float tj = (acc + b) + (c2 + d);
+    const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
+    float sum = (tj + t1) + (t2 + t3);
+    if (lane == 0)
+        for (int i = K & ~15; i < K; ++i) {
+            const float v = __half2float(x[i]);
+            const float v2 = v * v;
+            sum = sum + v2;
+        }
+    return sum;
+}
+
+__device__ __forceinline__ void c_unpack8(const uint4& raw, float v[8]) {
+    const __half2* hv = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float2 f = __half22float2(hv[i]);
+        v[2 * i] = f.x;
+        v[2 * i + 1] = f.y;
+    }
+}
+
+// RMSNorm (x * ns) * gamma of one group in place (src/model/cpu.rs:61-64).
+__device__ __forceinline__ void c_norm8(float v[8], const float* lg, int g, float ns) {
+    const float4 ga = *reinterpret_cast<const float4*>(lg + 8 * g);
+    const float4 gb = *reinterpret_cast<const float4*>(lg + 8 * g + 4);
+    const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (v[i] * ns) * gg[i];
+}
+
+__device__ __forceinline__ uint2 c_quant8(const float v[8], float im, bool fast, bool rne) {
+    int q[8];
+    if (fast && rne) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quant_finite<true>(v[i], im);
+    } else if (fast) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quant_finite<false>(v[i], im);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quant_one(v[i], im, rne);  // src/npu.rs:1107-1110
+    }
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w0 |= (uint32_t)(q[i] & 0xff) << (8 * i);
+        w1 |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+    }
+    return make_uint2(w0, w1);
+}
+
+// Helper waves: RMSNorm scale, per-token scale and the quantized rows of the stage
+// input (raw fp16 rows in LDS at off_x) into lds_q.  Same arithmetic as the GEMV
+// prologue.  h = helper thread index (0 .. kHT - 1).
+template <int MR>
+__device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStage& st, uint8_t* smem, int astride,
+                                           int h, ChainSync* sy, uint32_t& hk, float* s_inv, float* s_rows,
+                                           float (*s_red)[4], int* s_bad) {
+    const int hw = h >> 6, lane = h & 63;
+    const int M = p.M, K = st.K, ng = K >> 3;
+    const int xs = p.xstride >> 1;  // elements per LDS row
+    const __half* lx = reinterpret_cast<const __half*>(smem + p.off_x);
+    const float* lg = reinterpret_cast<const float*>(smem + p.off_g);
+    uint8_t* lds_q = smem;
+    const bool norm = st.gamma != nullptr;
+    // 1. RMSNorm scale per row (helper wave m computes row m), reference summation order
+    if (norm) {
+        if (hw < M) {
+            const __half* xrow = lx + hw * xs;
             float sum;
             if (st.flags & kFlagNormSeq)
-                sum = lane == 0 ? lds_sumsq_seq(xr, K) : 0.0f;  // src/ops/norm.rs:38
+                sum = lane == 0 ? lds_sumsq_seq(xrow, K) : 0.0f;  // src/ops/norm.rs:38
             else
-                sum = lds_sumsq_neon16(xr, K);  // src/model/cpu.rs:14-35
-            if (lane == 0) s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
+                sum = c_sumsq_neon16(xrow, K);  // src/model/cpu.rs:14-35
+            if (lane == 0) s_inv[hw] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
         }
-        __syncthreads();
+        helper_sync(sy, hk);
     }
-    float nscale[MR];
+    float nsc[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) nscale[m] = (st.gamma && m < M) ? s_inv[m] : 1.0f;
-    // 3. absmax (after the norm) and finiteness, per row
+    for (int m = 0; m < MR; ++m) nsc[m] = (norm && m < M) ? s_inv[m] : 1.0f;
+    // 2. absmax (after the norm) and finiteness, per row
     float mx[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
     int bad = 0;
-    for (int c = tid; c < M * ng; c += kChainThreads) {
-        const int m = c / ng, g = c - m * ng;
-        float v[8];
-        const uint4 raw = *reinterpret_cast<const uint4*>(lds_x + m * K + 8 * g);
-        const __half2* h = reinterpret_cast<const __half2*>(&raw);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float2 f = __half22float2(h[i]);
-            v[2 * i] = f.x;
-            v[2 * i + 1] = f.y;
+    for (int m = 0; m < MR; ++m) {
+        mx[m] = 0.0f;
+        if (m < M) {
+            for (int g = h; g < ng; g += kHT) {
+                float v[8];
+                c_unpack8(*reinterpret_cast<const uint4*>(lx + m * xs + 8 * g), v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) bad |= !__builtin_isfinite(v[i]);
+                if (norm) c_norm8(v, lg, g, nsc[m]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) mx[m] = fmaxf(mx[m], fabsf(v[i]));
+            }
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
-        float ns = 1.0f;
-#pragma unroll
-        for (int mm = 0; mm < MR; ++mm)
-            if (mm == m) ns = nscale[mm];
-        if (st.gamma) {
-            const float4 ga = *reinterpret_cast<const float4*>(st.gamma + 8 * g);
-            const float4 gb = *reinterpret_cast<const float4*>(st.gamma + 8 * g + 4);
-            const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gg[e];
-        }
-        float lm = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
-#pragma unroll
-        for (int mm = 0; mm < MR; ++mm)
-            if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         const float w = wave_max_nonneg(mx[m]);
-        if (lane == 0) s_red[wave][m] = w;
+        if (lane == 0) s_red[hw][m] = w;
     }
     const bool any_bad = __ballot(bad) != 0;
-    if (lane == 0) s_bad[wave] = any_bad;
-    lds_barrier();
-    // per-token scales, computed by every thread from the wave maxima
+    if (lane == 0) s_bad[hw] = any_bad;
+    helper_sync(sy, hk);
+    // 3. per-token scales, computed by every helper thread from the wave maxima
     int b = 0;
 #pragma unroll
-    for (int w = 0; w < kChainWaves; ++w) b |= s_bad[w];
+    for (int w = 0; w < kHW; ++w) b |= s_bad[w];
     float inv[MR];
     bool finite = true;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         float am = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kChainWaves; ++w) am = fmaxf(am, s_red[w][m]);
-        const float s = qscale_from_absmax(am);  // src/npu.rs:1101-1106
-        finite &= __builtin_isfinite(s);
-        inv[m] = 1.0f / s;
-        if (tid == 0 && m < M) s_rows[m] = s;
+        for (int w = 0; w < kHW; ++w) am = fmaxf(am, s_red[w][m]);
+        const float sc = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+        finite &= __builtin_isfinite(sc);
+        inv[m] = 1.0f / sc;
+        if (h == 0 && m < M) s_rows[m] = sc;
     }
-    if (tid == 0 && b && blockIdx.x == 0) atomicOr(p.err, 1u);
+    if (b && blockIdx.x == 0 && h == 0) atomicOr(p.err, 1u);
     // 4. quantize into LDS (k order for both widths); a finite row (the usual case)
     // takes the short rounding sequence
     const bool rne = (st.flags & kFlagRne) != 0;
     const bool fast = !b && finite;
-    for (int c = tid; c < M * ng; c += kChainThreads) {
-        const int m = c / ng, g = c - m * ng;
-        float v[8];
-        const uint4 raw = *reinterpret_cast<const uint4*>(lds_x + m * K + 8 * g);
-        const __half2* h = reinterpret_cast<const __half2*>(&raw);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float2 f = __half22float2(h[i]);
-            v[2 * i] = f.x;
-            v[2 * i + 1] = f.y;
+    for (int m = 0; m < MR; ++m) {
+        if (m < M) {
+            for (int g = h; g < ng; g += kHT) {
+                float v[8];
+                c_unpack8(*reinterpret_cast<const uint4*>(lx + m * xs + 8 * g), v);
+                if (norm) c_norm8(v, lg, g, nsc[m]);
+                *reinterpret_cast<uint2*>(lds_q + m * astride + 8 * g) = c_quant8(v, inv[m], fast, rne);
+            }
+            // zeros in [K, Kp): a previous stage may have left a longer row here
+            for (int k = K + h * 8; k < st.Kp; k += kHT * 8)
+                *reinterpret_cast<uint2*>(lds_q + m * astride + k) = make_uint2(0, 0);
         }
-        if (st.gamma) {
-            float ns = 1.0f;
-#pragma unroll
-            for (int mm = 0; mm < MR; ++mm)
-                if (mm == m) ns = nscale[mm];
-            const float4 ga = *reinterpret_cast<const float4*>(st.gamma + 8 * g);
-            const float4 gb = *reinterpret_cast<const float4*>(st.gamma + 8 * g + 4);
-            const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gg[e];
-        }
-        float im = 1.0f;
-#pragma unroll
-        for (int mm = 0; mm < MR; ++mm)
-            if (mm == m) im = inv[mm];
-        int q[8];
-        if (fast && rne) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = quant_finite<true>(v[e], im);
-        } else if (fast) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = quant_finite<false>(v[e], im);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
-        }
-        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
-            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-        }
-        *reinterpret_cast<uint2*>(lds_q + m * astride + 8 * g) = make_uint2(w0, w1);
     }
-    // zero the K..Kp tail of each row and the whole zero row M
-    for (int m = 0; m < M; ++m)
-        for (int k = K + tid * 8; k < st.Kp; k += kChainThreads * 8)
-            *reinterpret_cast<uint2*>(lds_q + m * astride + k) = make_uint2(0, 0);
-    for (int k = tid * 16; k < st.Kp; k += kChainThreads * 16)
-        *reinterpret_cast<uint4*>(lds_q + M * astride + k) = make_uint4(0, 0, 0, 0);
-    __syncthreads();
+    helper_sync(sy, hk);
 }
 
-// All rounds of one stage for this workgroup.  Returns the number of items done.
-template <int BITS, bool SWIGLU, int MR>
-__device__ int chain_stage(const ChainParams& p, const ChainStage& st, int s, uint8_t* smem, float* s_rows,
-                           float* s_inv, float (*s_red)[4], int* s_bad) {
-    constexpr int KS = BITS == 4 ? 256 : 128;
-    constexpr int LIVE_LANES = 16 * ((MR + 3) / 4);
-    constexpr int REGS = MR < 4 ? MR : 4;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int G = gridDim.x;
-    const int b = blockIdx.x;
-    const int n_items = st.groups > b ? (st.groups - 1 - b) / G + 1 : 0;
-    const int steps = st.Kp / KS;
-    const int Nh = st.N >> 1;
-    const int astride = p.kp_max + 16;
-    uint8_t* lds_q = smem;
-    int* red = reinterpret_cast<int*>(smem + p.lds_q_bytes);
-    __half* lds_x = reinterpret_cast<__half*>(smem + p.lds_q_bytes + p.lds_red_bytes);
+// I/O wave, after the products: dequant / SiLU-gate / residual epilogue of this
+// workgroup's outputs, fp16 device-coherent stores, then the completion flag.
+template <int BITS, bool SW, int MR>
+__device__ __forceinline__ void c_io_epilogue(const ChainParams& p, const ChainStage& st, int s, int b, int n_it,
+                                              uint32_t e, uint8_t* smem, const float* s_rows) {
+    const int lane = threadIdx.x & 63, M = p.M;
+    int* accg = reinterpret_cast<int*>(smem + p.off_acc);
+    int* accu = accg + p.ipw_max * 16 * MR;
+    const float* lsc = reinterpret_cast<const float*>(smem + p.off_sc);
+    const float* lr = reinterpret_cast<const float*>(smem + p.off_res);
+    const int sc_up = p.ipw_max * 16;
     const bool last = s == p.n_stages - 1;
-    const bool from_x = st.in == nullptr;
-    const __half* in = from_x ? p.x + st.x_offset : st.in;
-    const int64_t ld_in = from_x ? p.ldx : st.ld_in;
-    _Float16* out = last ? p.y : st.out;
+    uint16_t* out = reinterpret_cast<uint16_t*>(last ? p.y : st.out);
     const int64_t ld_out = last ? p.ldy : st.ld_out;
-    const int m_lane = lane & 15;
-    const bool live = m_lane < p.M;
-
-    if (n_items == 0) return 0;
-    for (int r = 0; r < n_items; r += 4) {
-        const int nr = min(4, n_items - r);
-        const int wpi = kChainWaves / nr;
-        const int item = wave / wpi;
-        const bool active = item < nr;
-        const int wave_in = wave - item * wpi;
-        const int g = b + (r + min(item, nr - 1)) * G;
-        const int r0 = 16 * g;
-        const uint8_t* wg = st.W + (int64_t)(r0 + (lane & 15)) * st.wrow + (lane >> 4) * 16;
-        const uint8_t* wu = SWIGLU ? st.W + (int64_t)(Nh + r0 + (lane & 15)) * st.wrow + (lane >> 4) * 16 : nullptr;
-        ChainBuf<SWIGLU> b0, b1;
-        int base = wave_in;
-        if (active) chain_load<BITS, SWIGLU>(b0, wg, wu, base, wpi, steps);
-        if (r == 0) {
-            // first round: the weights above are in flight while the stage input resolves
-            if (s > 0) chain_wait(p, p.counters + (s - 1), (uint32_t)p.stages[s - 1].groups);
-            chain_prologue<BITS, MR>(p, st, in, ld_in, !from_x, lds_q, astride, lds_x, s_rows, s_inv, s_red, s_bad);
-        }
-        v4i ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-        if (active) {
-            const uint8_t* arow = lds_q + (live ? m_lane : p.M) * astride + (lane >> 4) * (BITS == 4 ? 32 : 16);
-            const int span = wpi * kChainBatch;
-            while (base < steps) {
-                const int nb = base + span;
-                if (nb < steps) chain_load<BITS, SWIGLU>(b1, wg, wu, nb, wpi, steps);
-                chain_compute<BITS, SWIGLU>(ag, au, b0, arow, base, wpi, steps);
-                base = nb;
-                if (base >= steps) break;
-                const int nb2 = base + span;
-                if (nb2 < steps) chain_load<BITS, SWIGLU>(b0, wg, wu, nb2, wpi, steps);
-                chain_compute<BITS, SWIGLU>(ag, au, b1, arow, base, wpi, steps);
-                base = nb2;
+    for (int idx = lane; idx < n_it * 16 * MR; idx += 64) {
+        const int ch = idx / MR, m = idx - ch * MR;
+        const int i = ch >> 4, n = ch & 15;
+        if (m < M && n < c_width(st, b, i)) {
+            const int c = c_first(st, b, i) + n;
+            const int vg = accg[idx];
+            const int a_g = BITS == 4 ? (vg >> 4) : vg;  // exact: W4 sums carry a factor 16
+            float o = ((float)a_g * s_rows[m]) * lsc[ch];  // src/npu.rs:1117
+            if constexpr (SW) {
+                const int vu = accu[idx];
+                const int a_u = BITS == 4 ? (vu >> 4) : vu;
+                const float up = ((float)a_u * s_rows[m]) * lsc[sc_up + ch];
+                o = silu_gate(o, up);  // src/npu.rs:1202-1208
+            } else if (st.res_kind) {
+                // src/model/dense.rs:486-489: hidden + projected * residual_multiplier
+                const float pr = o * st.rmult;
+                o = lr[idx] + pr;
             }
+            const _Float16 h = f16_of_f32(o);
+            __hip_atomic_store(out + (int64_t)m * ld_out + c, __builtin_bit_cast(uint16_t, h), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
-        // cross-wave reduction of each item's partial sums, then the epilogue
-        if (active && lane < LIVE_LANES) {
-#pragma unroll
-            for (int i = 0; i < REGS; ++i) {
-                red[(wave * LIVE_LANES + lane) * REGS + i] = ag[i];
-                if constexpr (SWIGLU) red[kChainWaves * LIVE_LANES * REGS + (wave * LIVE_LANES + lane) * REGS + i] = au[i];
-            }
-        }
-        __syncthreads();
-        if (tid < nr * 16 * p.M) {
-            const int j = tid / (16 * p.M), rem = tid - j * 16 * p.M;
-            const int m = rem >> 4, n = rem & 15;
-            const int src = (16 * (m >> 2) + n) * REGS + (m & 3);
-            int vg = 0, vu = 0;
-            for (int w = j * wpi; w < (j + 1) * wpi; ++w) {
-                vg += red[w * LIVE_LANES * REGS + src];
-                if constexpr (SWIGLU) vu += red[kChainWaves * LIVE_LANES * REGS + w * LIVE_LANES * REGS + src];
-            }
-            const int cg = 16 * (b + (r + j) * G) + n;
-            const int ncols = SWIGLU ? Nh : st.N;
-            if (cg < ncols) {
-                const int a_g = BITS == 4 ? (vg >> 4) : vg;  // exact: W4 sums carry a factor 16
-                float o = ((float)a_g * s_rows[m]) * st.wscale[cg];  // src/npu.rs:1117
-                if constexpr (SWIGLU) {
-                    const int a_u = BITS == 4 ? (vu >> 4) : vu;
-                    const float up = ((float)a_u * s_rows[m]) * st.wscale[Nh + cg];
-                    o = silu_gate(o, up);  // src/npu.rs:1202-1208
-                } else if (st.res_kind) {
-                    // src/model/dense.rs:486-489: hidden + projected * residual_multiplier; an
-                    // earlier stage's rows are read device-coherently like a stage input
-                    const float pr = o * st.rmult;
-                    float hv;
-                    if (st.res_kind == 1) {
-                        hv = __half2float(p.x[(int64_t)m * p.ldx + st.res_x_offset + cg]);
-                    } else {
-                        const uint16_t bits = __hip_atomic_load(reinterpret_cast<const uint16_t*>(st.res) + (int64_t)m * st.ld_res + cg,
-                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        hv = (float)__builtin_bit_cast(_Float16, bits);
-                    }
-                    o = hv + pr;
-                }
-                const _Float16 h = f16_of_f32(o);
-                __hip_atomic_store(reinterpret_cast<uint16_t*>(out) + (int64_t)m * ld_out + cg,
-                                   __builtin_bit_cast(uint16_t, h), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        __syncthreads();  // the reduction area is reused by the next round
+        accg[idx] = 0;
+        if constexpr (SW) accu[idx] = 0;
     }
-    return n_items;
+    if (!last) {
+        wait_all_memory();  // this wave's coherent output stores have completed
+        if (lane == 0)
+            __hip_atomic_store(p.flags + (int64_t)s * kChainFlagStride + b, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The helper waves' part of stage s.
+template <int BITS, bool SW, int MR>
+__device__ __forceinline__ void c_stage_helpers(const ChainParams& p, int s, uint32_t e, uint8_t* smem, ChainSync* sy,
+                                                uint32_t& hk, float* s_inv, float* s_rows, float (*s_red)[4],
+                                                int* s_bad) {
+    const ChainStage st = c_desc(p, s);
+    const int b = blockIdx.x;
+    const int h = threadIdx.x - 64 * kCW;
+    const bool io = h < 64;
+    const int n_it = c_items(st, b);
+    if (io) c_io_input<SW, MR>(p, st, s, b, n_it, e, smem, sy);
+    helper_sync(sy, hk);
+    c_prologue<MR>(p, st, smem, p.kp_max + 16, h, sy, hk, s_inv, s_rows, s_red, s_bad);
+    if (io) {
+        if (h == 0) __hip_atomic_store(&sy->rows_ready, (uint32_t)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        lds_wait_ge(&sy->done, (uint32_t)(kCW * (s + 1)));  // every compute wave has added its sums
+        c_io_epilogue<BITS, SW, MR>(p, st, s, b, n_it, e, smem, s_rows);
+    }
+}
+
+// A compute wave's part of stage s.
+template <int MR>
+__device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i (&buf)[kNB], uint8_t* smem,
+                                                ChainSync* sy) {
+    const ChainStage st = c_desc(p, s);
+    const int wave = c_wave(), b = blockIdx.x;
+    const int astride = p.kp_max + 16;
+    const int E = c_row_items(st, c_items(st, b)) * st.steps;
+    int* accg = reinterpret_cast<int*>(smem + p.off_acc);
+    int* accu = accg + p.ipw_max * 16 * MR;
+    lds_wait_ge(&sy->rows_ready, (uint32_t)(s + 1));
+    // the host keeps every stage within one load of the compute waves (E <= kCW * kCMaxE)
+    const int f0 = E * wave / kCW, f1 = E * (wave + 1) / kCW;
+    c_compute<MR>(buf, st, b, f0, f1 - f0, smem, astride, p.M, accg, accu);
+    wait_lds();  // the sums are in LDS before this wave counts itself done
+    if ((threadIdx.x & 63) == 0) atomicAdd(&sy->done, 1u);
+    if (s + 1 < p.n_stages) {
+        // The next stage's weight loads wait until its input rows are in LDS.  Loads in
+        // flight during the exchange sit ahead of the exchange's own loads and stores in
+        // this CU's memory pipeline: issued right after the products, or half of them
+        // then, the 36-layer stack ran 1.2x / 1.13x slower than issued here.
+        lds_wait_ge(&sy->io_mark, (uint32_t)(2 * s + 2));
+        c_load_stage<0, kCMaxE>(p, s + 1, buf);
+    }
 }
 
 template <int MR>
-__global__ __launch_bounds__(kChainThreads) void chain_kernel(ChainParams p) {
+__global__ __launch_bounds__(kCT) void chain_kernel(ChainParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_rows[4], s_inv[4];
-    __shared__ float s_red[kChainWaves][4];
-    __shared__ int s_bad[kChainWaves];
-    for (int s = 0; s < p.n_stages; ++s) {
-        const ChainStage& st = p.stages[s];
-        const bool sw = (st.flags & kFlagSwiglu) != 0;
-        int done;
-        if (st.bits == 4)
-            done = sw ? chain_stage<4, true, MR>(p, st, s, smem, s_rows, s_inv, s_red, s_bad)
-                      : chain_stage<4, false, MR>(p, st, s, smem, s_rows, s_inv, s_red, s_bad);
-        else
-            done = sw ? chain_stage<8, true, MR>(p, st, s, smem, s_rows, s_inv, s_red, s_bad)
-                      : chain_stage<8, false, MR>(p, st, s, smem, s_rows, s_inv, s_red, s_bad);
-        if (done > 0) {
-            wait_all_memory();  // this wave's coherent output stores have completed
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                const uint32_t old = atomicAdd(p.counters + s, (uint32_t)done);
-                if (s == p.n_stages - 1 && old + done == (uint32_t)st.groups) {
-                    // every item of every stage is complete: reset for the next launch
-                    for (int i = 0; i < p.n_stages; ++i)
-                        __hip_atomic_store(p.counters + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+    __shared__ float s_inv[4], s_rows[4];
+    __shared__ float s_red[kHW][4];
+    __shared__ int s_bad[kHW];
+    __shared__ ChainSync sy;
+    const int tid = threadIdx.x, b = blockIdx.x;
+    const int astride = p.kp_max + 16;
+    // zero rows of the quantized activations (row M is the MFMA's zero row) and the sums
+    for (int i = tid * 16; i < (MR + 1) * astride; i += kCT * 16)
+        *reinterpret_cast<uint4*>(smem + i) = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < 2 * p.ipw_max * 16 * MR; i += kCT) reinterpret_cast<int*>(smem + p.off_acc)[i] = 0;
+    if (tid == 0) {
+        sy.rows_ready = 0;
+        sy.done = 0;
+        sy.helpers = 0;
+        sy.io_mark = 0;
+    }
+    __syncthreads();  // the only workgroup barrier
+    if (tid < 64 * kCW) {
+        v4i buf[kNB];
+        c_load_stage<0, kCMaxE>(p, 0, buf);
+        for (int s = 0; s < p.n_stages; ++s) {
+            c_stage_compute<MR>(p, s, buf, smem, &sy);
+        }
+    } else {
+        // the helpers' instructions (the exchange between stages) issue ahead of the
+        // compute waves' weight loads
+        __builtin_amdgcn_s_setprio(2);
+        const bool io = tid < 64 * (kCW + 1);
+        uint32_t e = 0, hk = 0;
+        if (io) e = __hip_atomic_load(p.epochs + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+        for (int s = 0; s < p.n_stages; ++s) {
+            const ChainStage st = c_desc(p, s);
+            const bool sw = (st.flags & kFlagSwiglu) != 0;
+            if (st.bits == 4) {
+                if (sw)
+                    c_stage_helpers<4, true, MR>(p, s, e, smem, &sy, hk, s_inv, s_rows, s_red, s_bad);
+                else
+                    c_stage_helpers<4, false, MR>(p, s, e, smem, &sy, hk, s_inv, s_rows, s_red, s_bad);
+            } else {
+                if (sw)
+                    c_stage_helpers<8, true, MR>(p, s, e, smem, &sy, hk, s_inv, s_rows, s_red, s_bad);
+                else
+                    c_stage_helpers<8, false, MR>(p, s, e, smem, &sy, hk, s_inv, s_rows, s_red, s_bad);
             }
         }
+        if (io && (tid & 63) == 0) __hip_atomic_store(p.epochs + b, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-size_t chain_lds_bytes(int max_rows, int kp_max, int k_max, size_t* q_bytes, size_t* red_bytes) {
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+size_t chain_lds_layout(int max_rows, int kp_max, int k_max, int kg_max, int ipw_max, ChainParams* p) {
     const int mr = max_rows <= 1 ? 1 : 4;
-    const size_t q = (size_t)(mr + 1) * (kp_max + 16);
-    const size_t red = (size_t)2 * kChainWaves * 16 * (mr < 4 ? mr : 4) * sizeof(int);
-    const size_t x = (size_t)mr * k_max * sizeof(__half);
-    *q_bytes = (q + 15) & ~(size_t)15;
-    *red_bytes = (red + 15) & ~(size_t)15;
-    return *q_bytes + *red_bytes + x;
+    size_t off = align_up((size_t)(mr + 1) * (kp_max + 16), 16);
+    p->xstride = (int)align_up((size_t)k_max * 2, 1024);
+    p->off_x = (int)off;
+    off += (size_t)mr * p->xstride;
+    p->off_g = (int)off;
+    off += align_up((size_t)kg_max * 4, 1024);
+    p->off_acc = (int)off;
+    off += (size_t)2 * ipw_max * 16 * mr * 4;
+    p->off_sc = (int)off;
+    off += (size_t)2 * ipw_max * 16 * 4;
+    p->off_res = (int)off;
+    off += (size_t)ipw_max * 16 * mr * 4;
+    p->ipw_max = ipw_max;
+    return off;
 }
 
 int chain_resident_per_cu(int max_rows, size_t lds) {
@@ -423,7 +699,7 @@ int chain_resident_per_cu(int max_rows, size_t lds) {
     const void* f = max_rows <= 1 ? reinterpret_cast<const void*>(&chain_kernel<1>)
                                   : reinterpret_cast<const void*>(&chain_kernel<4>);
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kChainThreads, lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kCT, lds) != hipSuccess) return 0;
     return n;
 }
 
@@ -432,12 +708,12 @@ hipError_t launch_chain(const ChainParams& p, int grid, size_t lds, hipStream_t 
         static const hipError_t a1 = hipFuncSetAttribute(reinterpret_cast<const void*>(&chain_kernel<1>),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds);
         if (a1 != hipSuccess) return a1;
-        chain_kernel<1><<<grid, kChainThreads, lds, stream>>>(p);
+        chain_kernel<1><<<grid, kCT, lds, stream>>>(p);
     } else {
         static const hipError_t a4 = hipFuncSetAttribute(reinterpret_cast<const void*>(&chain_kernel<4>),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds);
         if (a4 != hipSuccess) return a4;
-        chain_kernel<4><<<grid, kChainThreads, lds, stream>>>(p);
+        chain_kernel<4><<<grid, kCT, lds, stream>>>(p);
     }
     return hipGetLastError();
 }

@@ -7,23 +7,33 @@
 
 namespace qlin {
 
+constexpr int kChainComputeWaves = 4;  // waves that stream weights (one per SIMD)
+constexpr int kChainHelperWaves = 4;   // waves that exchange rows and quantize them
+constexpr int kChainThreadsPerBlock = 64 * (kChainComputeWaves + kChainHelperWaves);
+constexpr int kChainMaxLds = 159 * 1024;  // dynamic LDS cap: 160 KiB less the static words
+constexpr int kChainBufRegs = 40;         // 16-byte weight registers per compute lane
+constexpr int kChainFlagStride = 256;     // flag words per stage (>= grid, multiple of 256)
+
 struct ChainStage {
     const uint8_t* W;       // packed weights [Np, wrow]
     const float* wscale;    // [Np]
     int64_t wrow;
     int bits, K, Kp, N, Np;
     int flags;              // kFlagSwiglu | kFlagRne | kFlagNormSeq
-    int groups;             // items: 16-channel groups ((SwiGLU ? N/2 : Np) / 16)
+    int ncols;              // output columns: N, or N/2 with SwiGLU
+    int iw, ipw;            // output channels per item (1..16), items per workgroup
+    int steps;              // 128-byte weight steps per row: Kp / 256 (W4) or Kp / 128 (W8)
     const float* gamma;     // RMSNorm weights [K] or null
     float eps;
     const __half* in;       // input rows: an earlier stage's output, or null for the chain input
     int64_t ld_in;
     int x_offset;           // first chain-input column read (when in is null)
-    _Float16* out;          // stage output rows [rows, N or N/2]
+    _Float16* out;          // stage output rows [rows, ncols]
     int64_t ld_out;
     // residual update (res_kind 1: the chain input from column res_x_offset; 2: an earlier
     // stage's output at res): out = R + y * rmult
     int res_kind;
+    int res_stage;          // stage whose output res points into (-1: the chain input)
     const __half* res;
     int64_t ld_res;
     int res_x_offset;
@@ -38,17 +48,26 @@ struct ChainParams {
     int64_t ldx;
     _Float16* y;
     int64_t ldy;
-    uint32_t* counters;        // [n_stages], zero at rest
+    uint32_t* flags;           // [n_stages][kChainFlagStride]: launch epoch of each workgroup's
+                               // finished part of each stage
+    uint32_t* epochs;          // [grid]: launches each workgroup has completed
     uint32_t* err;             // bit 0: non-finite input; bit 1: a stage wait gave up
     int spin_limit;
     int kp_max;                // largest Kp over the stages
-    int lds_q_bytes, lds_red_bytes;
+    int ipw_max;               // largest items per workgroup over the stages
+    // LDS carve-up, byte offsets into the dynamic area
+    int off_x, xstride;        // raw input rows (fp16), row stride in bytes (multiple of 1 KiB)
+    int off_g;                 // RMSNorm weights (f32)
+    int off_acc;               // int32 sums [2][ipw_max * 16][MR]
+    int off_sc;                // per-channel scales [2][ipw_max * 16]
+    int off_res;               // residual rows [ipw_max * 16][MR] (f32)
 };
 
-size_t chain_lds_bytes(int max_rows, int kp_max, int k_max, size_t* q_bytes, size_t* red_bytes);
+// LDS bytes of a chain (and the carve-up written into p).
+size_t chain_lds_layout(int max_rows, int kp_max, int k_max, int kg_max, int ipw_max, ChainParams* p);
 hipError_t launch_chain(const ChainParams& p, int grid, size_t lds, hipStream_t stream);
 int chain_resident_per_cu(int max_rows, size_t lds);  // workgroups of the chain kernel per CU
-constexpr int kChainThreadsPerBlock = 512;
-constexpr int kChainMaxLds = 159 * 1024;  // dynamic LDS cap: 160 KiB less the static words
+// Largest weight steps one workgroup round takes for a stage of this kind.
+int chain_round_capacity();
 
 }  // namespace qlin

@@ -13,7 +13,7 @@ import torch
 
 from open_rknpu2_lm_infer_amd import qlinear as ql
 from open_rknpu2_lm_infer_amd import synth
-from open_rknpu2_lm_infer_amd._lib import QLIN_ERR_NONFINITE, QLIN_ERR_PARAM, QLIN_ERR_UNSUPPORTED, QlinError
+from open_rknpu2_lm_infer_amd._lib import QLIN_ERR_NONFINITE, QLIN_ERR_PARAM, QlinError
 from tests.test_gpu_parity import check_outputs, f16_bits, oracle_linear
 
 pytestmark = pytest.mark.gpu
@@ -32,6 +32,17 @@ def linear(bits, K, N, seed, stack=False):
     packed, codes, sc = synth.make_linear(N, K, bits, seed, stack=stack)
     w = ql.Weights.from_packed_device(bits, K, N, packed.to(DEV), sc.to(DEV))
     return w, codes.numpy(), sc.numpy()
+
+
+def linear_unit(bits, K, N, seed):
+    """A linear whose outputs keep an O(1) magnitude through SiLU-gate stages: scales
+    1 / (code std * sqrt(K)) so short chains of small, oddly shaped stages stay finite."""
+    codes = synth.codes(N, K, bits, seed)
+    std = 4.6 if bits == 4 else 73.3
+    sc = (torch.rand((N,), generator=synth.gen(seed + 7, "cpu")) * 0.4 + 0.8) / (std * K ** 0.5)
+    packed = synth.pack_w4(codes) if bits == 4 else codes.contiguous()
+    w = ql.Weights.from_packed_device(bits, K, N, packed.to(DEV), sc.float().to(DEV))
+    return w, codes.numpy(), sc.float().numpy()
 
 
 def stage_inputs(chain, stages, x, y, rows):
@@ -126,8 +137,8 @@ def test_chain_qwen_layer(ws, rows):
 
 
 def test_chain_two_layers_repeat(ws):
-    """Eight stages; three launches in a row give identical results (the counters
-    reset themselves at the end of each launch)."""
+    """Eight stages; three launches in a row give identical results (the completion
+    flags of one launch never satisfy the waits of the next)."""
     gam = [synth.gamma(synth.HIDDEN, seed=920 + i).to(DEV) for i in range(4)]
     s0, h0 = qwen_layer_stages(0, gam[:2])
     s1, h1 = qwen_layer_stages(1, gam[2:])
@@ -172,12 +183,12 @@ def test_chain_graph_replay():
 def test_chain_rejects_bad_stages():
     w_a = linear(4, 256, 512, 940)[0]
     w_b = linear(8, 512, 256, 941)[0]
-    w_c = linear(4, 256, 96, 942)[0]  # N % 64 != 0
+    w_c = linear(4, 256, 97, 942)[0]  # odd N: no SiLU-gate pairing
     cases = [
         ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=0, offset=4)], QLIN_ERR_PARAM),  # offset % 8
         ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=1, offset=0)], QLIN_ERR_PARAM),  # not earlier
         ([dict(weights=w_a, input=-1, offset=0), dict(weights=w_b, input=0, offset=8)], QLIN_ERR_PARAM),  # past the end
-        ([dict(weights=w_c, flags=ql.QLIN_SWIGLU, input=-1, offset=0)], QLIN_ERR_UNSUPPORTED),
+        ([dict(weights=w_c, flags=ql.QLIN_SWIGLU, input=-1, offset=0)], QLIN_ERR_PARAM),
         ([dict(weights=w_a, input=0, offset=0)], QLIN_ERR_PARAM),  # stage 0 must read the input
     ]
     for stages, rc in cases:
@@ -226,4 +237,56 @@ def test_chain_wait_give_up_and_recover(ws):
         check_against_single(ws, chain, stages, x, y, 1)
     with pytest.raises(QlinError):
         chain.set_wait_limit(-1)
+    chain.close()
+
+
+def test_chain_new_input_every_launch(oracle, ws):
+    """Five launches with a different input each, eager and from a graph whose input
+    buffer is refilled between replays: every stage of every launch equals the single
+    linears on what it consumed, so no stage read a stale row of an earlier launch."""
+    gam = [synth.gamma(synth.HIDDEN, seed=960 + i).to(DEV) for i in range(4)]
+    s0, h0 = qwen_layer_stages(0, gam[:2])
+    s1, h1 = qwen_layer_stages(1, gam[2:])
+    stages = s0 + s1
+    chain = ql.Chain(stages, max_rows=4)
+    x = torch.empty((3, synth.HIDDEN), dtype=torch.float16, device=DEV)
+    y = torch.empty((3, stages[-1]["weights"].N), dtype=torch.float16, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    x.copy_(synth.activations(3, synth.HIDDEN, seed=969, device=DEV))
+    chain.run(x, out=y)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        chain.run(x, out=y)
+    for launch in range(5):
+        x.copy_(synth.activations(3, synth.HIDDEN, seed=970 + launch, device=DEV))
+        if launch % 2:
+            g.replay()
+        else:
+            chain.run(x, out=y)
+        torch.cuda.synchronize()
+        assert chain.status() == 0
+        check_against_single(ws, chain, stages, x, y, 3)
+    chain.close()
+
+
+def test_chain_swiglu_any_even_width(oracle, ws):
+    """SiLU-gate stages whose half width is not a multiple of 16 or 64 (96 -> 48, 2 x 1000
+    -> 1000): output channels are dealt to workgroups one by one, so any even N works."""
+    wa = linear_unit(4, 512, 96, 980)
+    wb = linear_unit(8, 48, 2000, 981)
+    wc = linear_unit(4, 1000, 256, 982)
+    stages = [
+        dict(weights=wa[0], flags=ql.QLIN_SWIGLU, input=-1, offset=0),
+        dict(weights=wb[0], flags=ql.QLIN_SWIGLU, input=0, offset=0),
+        dict(weights=wc[0], flags=0, input=1, offset=0),
+    ]
+    chain = ql.Chain(stages, max_rows=2)
+    x = synth.activations(2, 512, seed=983, device=DEV)
+    y = chain.run(x)
+    torch.cuda.synchronize()
+    assert chain.status() == 0
+    ins, outs = check_against_single(ws, chain, stages, x, y, 2)
+    for s, (st, host) in enumerate(zip(stages, (wa, wb, wc))):
+        expect = oracle_linear(oracle, ins[s].cpu(), host[1], host[2], bool(st["flags"] & ql.QLIN_SWIGLU))
+        check_outputs(oracle, outs[s], expect, bool(st["flags"] & ql.QLIN_SWIGLU), torch.float16)
     chain.close()
