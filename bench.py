@@ -202,6 +202,21 @@ def main():
                 gemm_only(p, i)
         torch.cuda.synchronize()
         log("M=512 GEMMs done")
+        # and the M=4096 gate_up GEMM (quantized Student-t rows in, SiLU-gate epilogue)
+        M4k = 4096
+        K, N = synth.LAYER[2][1], synth.LAYER[2][2]
+        ws4k = ql.Workspace(M4k, K, N)
+        q4k, s4k = ql.quantize(synth.activations(M4k, K, seed=50102, device=dev, dist="student_t3"),
+                               ldq=layers[0][2].K_padded)
+        o4k = torch.empty((M4k, N // 2), dtype=torch.float16, device=dev)
+        lib = _lib.load()
+        for i in range(8):
+            ql.check(lib.qlin_run_quantized(ws4k.handle, layers[i % L][2].handle, M4k, ql._ptr(q4k), q4k.stride(0),
+                                            ql._ptr(s4k), ql._ptr(o4k), ql.QLIN_F16, o4k.stride(0), ql.QLIN_SWIGLU,
+                                            ql._stream()), "qlin_run_quantized")
+        torch.cuda.synchronize()
+        ws4k.close()
+        log("M=4096 gate_up GEMMs done")
         return
 
     # ---------------------------------------------------------------- headline: decode layer

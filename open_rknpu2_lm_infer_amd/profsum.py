@@ -36,17 +36,31 @@ def kernel_stats(path, match=None):
     return out
 
 
-def pmc_means(path, match=None):
-    """{kernel name: {counter: mean value per dispatch}} (values summed over instances)."""
+def pmc_means(path, match=None, chunk=0):
+    """{kernel name [grid]: {counter: mean value per dispatch}} (values summed over
+    instances), one entry per kernel and grid size.  chunk > 0 splits each entry into
+    consecutive runs of that many dispatches (in dispatch order), labelled #0, #1, ...:
+    a program that launches the same kernel and grid for different shapes one shape
+    after another gets one entry per shape."""
     con = _con(path)
     rows = con.execute(
-        "select name, dispatch_id, counter_name, sum(counter_value) from pmc_events "
-        "group by name, dispatch_id, counter_name").fetchall()
+        "select P.name, K.grid_x / max(K.workgroup_x, 1), P.dispatch_id, P.counter_name, sum(P.counter_value) "
+        "from pmc_events P join kernels K on K.dispatch_id = P.dispatch_id "
+        "group by P.name, K.grid_x, P.dispatch_id, P.counter_name order by P.dispatch_id").fetchall()
+    order = {}
+    for name, wgs, disp, _, _ in rows:
+        ids = order.setdefault((name, wgs), [])
+        if not ids or ids[-1] != disp:
+            ids.append(disp)
+    rank = {(k, d): i for k, ids in order.items() for i, d in enumerate(ids)}
     acc = {}
-    for name, _, cn, v in rows:
+    for name, wgs, disp, cn, v in rows:
         if match and not re.search(match, name):
             continue
-        d = acc.setdefault(name, {}).setdefault(cn, [0.0, 0])
+        key = f"{name} [{wgs} workgroups]"
+        if chunk:
+            key += f" #{rank[((name, wgs), disp)] // chunk}"
+        d = acc.setdefault(key, {}).setdefault(cn, [0.0, 0])
         d[0] += v
         d[1] += 1
     return {k: {c: s / n for c, (s, n) in v.items()} for k, v in acc.items()}
@@ -72,6 +86,7 @@ def main(argv=None):
     ap.add_argument("--copy-match", default="copyBuffer")
     ap.add_argument("--copy-bytes", type=float)
     ap.add_argument("--md", action="store_true", help="stats as a markdown table with each kernel's share")
+    ap.add_argument("--chunk", type=int, default=0, help="pmc: split each kernel and grid into runs of N dispatches")
     a = ap.parse_args(argv)
     if a.what == "stats" and a.md:
         rows = kernel_stats(a.db, a.match)
@@ -88,7 +103,7 @@ def main(argv=None):
             print(f"{r['avg_us']:9.2f} us avg  {r['min_us']:8.2f} min  {r['max_us']:8.2f} max  n={r['dispatches']:6d}  "
                   f"wg={r['workgroups']}x{r['wg_size']} vgpr={r['vgpr']} lds={r['lds']}  {r['name'][:110]}")
     elif a.what == "pmc":
-        for name, d in pmc_means(a.db, a.match).items():
+        for name, d in pmc_means(a.db, a.match, a.chunk).items():
             print(name[:120])
             for c, v in sorted(d.items()):
                 print(f"    {c:32s} {v:16.2f}")
