@@ -21,7 +21,7 @@ the W8 lm_head, the M=4096 prefill layer with RMSNorm fused into the quantizatio
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
     python bench.py --mode kernel   # only the dominant kernel, for rocprofv3 --pmc passes
-    python bench.py --mode gemm     # only the M=512 GEMMs, for rocprofv3 --pmc passes
+    python bench.py --mode gemm     # only the M=512 GEMMs and the M=4096 gate_up GEMM, for --pmc passes
     python bench.py --mode copy     # a plain 256 MiB device copy, the counters' calibration
 
 roofline.traffic is read from profiles/gemv_gate_up_w4_m1_traffic.txt (written by
@@ -339,6 +339,7 @@ def main():
         log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM); "
             f"GEMM alone {us_g:.1f} us, {prefill[name]['gemm_tops']} TOPS")
     prefill_tops = tot_ops / (tot_us * 1e-6) / 1e12
+    prefill_gemm_tops = tot_ops / (tot_gemm_us * 1e-6) / 1e12
     dom_p = max(prefill, key=lambda n: prefill[n]["gemm_us"])
     dom_ops = 2.0 * M512 * dict((n, (K, N)) for n, K, N in synth.LAYER)[dom_p][0] * \
         dict((n, (K, N)) for n, K, N in synth.LAYER)[dom_p][1]
@@ -540,7 +541,7 @@ def main():
         "per_kernel_decode": per_kernel,
         "w8_gemv_2560": w8_line,
         "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
-                         "gemm_only_tops": round(tot_ops / (tot_gemm_us * 1e-6) / 1e12, 1),
+                         "gemm_only_tops": round(prefill_gemm_tops, 1),
                          "per_proj": prefill},
         "lm_head_w8_m1": head,
         "decode_stack_mixed": stack,
