@@ -74,6 +74,8 @@ struct GemmGeom {
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 word 3)
+constexpr int kSc1 = 16;                   // buffer cache policy: coherent at device scope (sc1)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t rows, int64_t ld) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(rows * ld), kBufferFlags);
@@ -368,15 +370,18 @@ __global__ __launch_bounds__(128 * WN) void gemm_kernel(GemmParams p) {
     }
 
     if (p.splits > 1) {
-        const int64_t base = (int64_t)tile * p.splits * G::REGS * G::THREADS;
-        int32_t* mine = p.part + base + (int64_t)z * G::REGS * G::THREADS;
+        // Each thread's 4 x NI accumulator fragments go out as 16-byte device-coherent
+        // stores, fragment-major ((i * NI + j) * THREADS + tid): a quarter of the memory
+        // instructions of one 4-byte store per register.
+        constexpr int SLICE = G::REGS * G::THREADS * 4;  // bytes of one split's partial tile
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            p.part + (int64_t)tile * p.splits * G::REGS * G::THREADS, (short)0, p.splits * SLICE, kBufferFlags);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < G::NI; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    store_coherent(mine + ((i * G::NI + j) * 4 + r) * G::THREADS + tid, acc[i][j][r]);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rp,
+                                                       ((i * G::NI + j) * G::THREADS + tid) * 16, z * SLICE, kSc1);
         wait_all_memory();
         __syncthreads();
         int* flag = reinterpret_cast<int*>(smem);  // the LDS stages are drained
@@ -385,14 +390,12 @@ __global__ __launch_bounds__(128 * WN) void gemm_kernel(GemmParams p) {
         if (!flag[0]) return;
         for (int zz = 0; zz < p.splits; ++zz) {
             if (zz == z) continue;
-            const int32_t* other = p.part + base + (int64_t)zz * G::REGS * G::THREADS;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < G::NI; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += load_coherent(other + ((i * G::NI + j) * 4 + r) * G::THREADS + tid);
+                    acc[i][j] += __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(rp, ((i * G::NI + j) * G::THREADS + tid) * 16, zz * SLICE, kSc1));
         }
         if (tid == 0) atomicExch(&p.counters[tile], 0u);
     }

@@ -381,6 +381,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
     }
 
+    // Threads holding two or more activation groups (long rows): every wave's activation
+    // loads enter the CU's memory queue before any wave's weight loads.  A barrier here
+    // without waiting for the loads; the down GEMV (K = 9728) 7.05 -> 6.35 us per launch.
+    // With one group per thread it measured slower (o 4.12 -> 4.22 us) and is skipped.
+    if constexpr (FUSED) {
+        if (nreg >= 2) issue_barrier();
+    }
+
     // ---- 2. first weight batch ---------------------------------------------------
     // lane rows past the item's width (or past the last channel) re-read its last row
     const int wrow_l = min(r0 + min(lane & 15, p.iw - 1), ncols - 1);
@@ -667,6 +675,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
         }
     } else {
         if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
+    }
+
+    // Threads holding two or more activation groups (long rows): every wave's activation
+    // loads enter the CU's memory queue before any wave's weight loads.  A barrier here
+    // without waiting for the loads; the down GEMV (K = 9728) 7.05 -> 6.35 us per launch.
+    // With one group per thread it measured slower (o 4.12 -> 4.22 us) and is skipped.
+    if constexpr (FUSED) {
+        if (nreg >= 2) issue_barrier();
     }
 
     // ---- 2. first weight batch ---------------------------------------------------

@@ -218,6 +218,8 @@ __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// A workgroup barrier that waits for no memory counter: orders instruction issue only.
+__device__ __forceinline__ void issue_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void store_coherent(int32_t* p, int32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
