@@ -681,12 +681,26 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
     int S = ov.gemm_splits;
     if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
     if (S <= 0) {
-        // split K until the grid covers the CUs, keeping >= 4 k tiles per split
-        // split-K's partial round trip costs more than a second resident workgroup
-        // per CU gains, so the target is one workgroup per CU
+        // Split K while the grid stays within one workgroup per CU (split-K's partial round
+        // trip costs more than a second resident workgroup per CU gains), keeping >= 4 k
+        // tiles per split, and take the count with the least estimated time: a split's
+        // longest k range at ~0.45 us per k tile, plus for a split tile ~1.5 us of round
+        // trips and its partials (written by every split, read by the last) at ~4.5 TB/s.
+        // Measured at M = 512: o (K = 4096, 80 tiles) 18.2 us with 2 splits, 18.9 with 3;
+        // down (K = 9728) 26.8 / 24.7 us.  Filling the CUs alone took 3 for both.
         const int target = ov.gemm_target_wgs > 0 ? ov.gemm_target_wgs : ws->cu_count;
-        S = (target + tiles / 2) / tiles;
-        S = std::min(S, std::max(1, ktiles / 4));
+        const int smax = std::max(1, std::min((target + tiles / 2) / tiles, ktiles / 4));
+        S = 1;
+        double best = 1e30;
+        for (int t = 1; t <= smax; ++t) {
+            const int per = ((ktiles + t - 1) / t + 1) & ~1;  // even k tiles per split
+            const double exch = t > 1 ? 1.5 + (2.0 * t - 1) * tiles * slice * 4.0 / 4.5e6 : 0.0;
+            const double est = 0.45 * per + exch;
+            if (est < best - 1e-9) {
+                best = est;
+                S = t;
+            }
+        }
     }
     S = std::max(1, std::min(S, ktiles));
     while (S > 1 && ((int64_t)tiles * S * slice > ws->part_ints || tiles > ws->n_counters)) --S;
