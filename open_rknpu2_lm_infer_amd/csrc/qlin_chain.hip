@@ -346,54 +346,10 @@ __device__ __forceinline__ void c_io_input(const ChainParams& p, const ChainStag
     if (lane == 0) __hip_atomic_store(&sy->io_mark, (uint32_t)(2 * s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Sum of squares of a row of K fp16 values in LDS, in the order of src/model/cpu.rs:14-35:
-// 16 fused-multiply-add chains (chain j takes elements j, j+16, ... in order), combined
-// lanewise as (a+b)+(c+d), then (t0+t1)+(t2+t3), then the scalar tail sum += v*v.  Lane j
-// of one wave runs chain j; the next eight elements' LDS reads are in flight while the
-// current eight FMAs run.  Result valid in lane 0.
-__device__ float c_sumsq_neon16(const __half* x, int K) {
-    const int lane = threadIdx.x & 63, j = lane & 15;
-    float acc = 0.0f;
-    if (lane < 16) {
-        const int nb = (K & ~15) >> 7;  // batches of 8 elements per chain (128 per batch)
-        const int n8 = nb << 7;
-        float a[8], c[8];
-        if (nb > 0) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) a[u] = __half2float(x[16 * u + j]);
-        }
-        for (int bt = 0; bt < nb; bt += 2) {
-            const int i = bt << 7;
-            if (bt + 1 < nb) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) c[u] = __half2float(x[i + 128 + 16 * u + j]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(a[u], a[u], acc);
-            if (bt + 1 >= nb) break;
-            if (bt + 2 < nb) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) a[u] = __half2float(x[i + 256 + 16 * u + j]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(c[u], c[u], acc);
-        }
-        for (int i = n8; i < (K & ~15); i += 16) {  // the last partial batch
-            const float v = __half2float(x[i + j]);
-            acc = __builtin_fmaf(v, v, acc);
-        }
-    }
-    const float b = __shfl(acc, j + 4, 64), c2 = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
-    const float tj = (acc + b) + (c2 + d);
-    const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
-    float sum = (tj + t1) + (t2 + t3);
-    if (lane == 0)
-        for (int i = K & ~15; i < K; ++i) {
-            const float v = __half2float(x[i]);
-            const float v2 = v * v;
-            sum = sum + v2;
-        }
-    return sum;
+// Sum of squares of a row of K fp16 values in LDS in the reference order (see
+// lds_sumsq_neon16): one wave, result in lane 0.
+__device__ __forceinline__ float c_sumsq_neon16(const __half* x, int K) {
+    return lds_sumsq_neon16(reinterpret_cast<const _Float16*>(x), K);
 }
 
 __device__ __forceinline__ void c_unpack8(const uint4& raw, float v[8]) {

@@ -155,25 +155,32 @@ __device__ float lds_sumsq_seq(const T* x, int K) {
 // Sum of squares of a row held in LDS, in the order of src/model/cpu.rs:14-35: 16
 // fused-multiply-add chains (chain j takes elements j, j+16, ... in order), combined
 // lanewise as (a+b)+(c+d), then (t0+t1)+(t2+t3), then the scalar tail sum += v*v.
-// Called by all 64 lanes of one wave; the result is valid in lane 0.  Each chain
-// issues the loads of 16 elements before their FMAs.
+// Called by all 64 lanes of one wave; the result is valid in lane 0.  Lane j runs
+// chain j 32 steps (512 elements of the row) per loop trip, all 32 reads of a trip
+// issued before its FMAs: with a loop of 16-element batches and a runtime K the reads
+// waited one batch at a time (2560 fp16 values: 1.9 -> 1.1-1.2 us).  fp16 values are
+// kept as fp16 so each conversion folds into its FMA (v_fma_mix_f32, exact).
 template <typename T>
 __device__ float lds_sumsq_neon16(const T* x, int K) {
     const int lane = threadIdx.x & 63, j = lane & 15;
     float acc = 0.0f;
     if (lane < 16) {
+        const T* c = x + j;
         const int n16 = K & ~15;
         int i = 0;
-        for (; i + 256 <= n16; i += 256) {
-            float v[16];
+        for (; i + 512 <= n16; i += 512) {
+            T v[32];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = lds_f32(x, i + 16 * u + j);
+            for (int u = 0; u < 32; ++u) v[u] = c[i + 16 * u];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(v[u], v[u], acc);
+            for (int u = 0; u < 32; ++u) {
+                const float f = (float)v[u];
+                acc = __builtin_fmaf(f, f, acc);
+            }
         }
         for (; i < n16; i += 16) {
-            const float v = lds_f32(x, i + j);
-            acc = __builtin_fmaf(v, v, acc);
+            const float f = (float)c[i];
+            acc = __builtin_fmaf(f, f, acc);
         }
     }
     const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
@@ -182,7 +189,7 @@ __device__ float lds_sumsq_neon16(const T* x, int K) {
     float sum = (tj + t1) + (t2 + t3);
     if (lane == 0)
         for (int i = K & ~15; i < K; ++i) {
-            const float v = lds_f32(x, i);
+            const float v = (float)x[i];
             const float v2 = v * v;
             sum = sum + v2;
         }
