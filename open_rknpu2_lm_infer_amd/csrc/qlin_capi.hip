@@ -41,7 +41,7 @@ struct QlinOverrides {
     int gemm_deep;        // QLIN_GEMM_DEEP, 0 / 1
     int gemm_wn;          // QLIN_GEMM_WN, 2 / 4
     int gemm_kernel;      // QLIN_GEMM_KERNEL: 16 forces the 16x16x64 kernel
-    int gemm_cfg;         // QLIN_GEMM_CFG: forces the 32x32x32 kernel with tile configuration 0..2
+    int gemm_cfg;         // QLIN_GEMM_CFG: forces the 32x32x32 kernel with tile configuration 0..3 (3: W4 only)
 };
 
 struct qlin_workspace {
@@ -644,12 +644,22 @@ struct GemmPlan {
 // Returns -1 for the 16x16x64 kernel, else the 32x32x32 tile configuration.
 int gemm_pick(const qlin_workspace* ws, const qlin_weights* w, int rows, bool sw) {
     if (ws->ov.gemm_kernel == 16) return -1;
-    if (ws->ov.gemm_cfg >= 0 && ws->ov.gemm_cfg <= 2) return ws->ov.gemm_cfg;
+    if (ws->ov.gemm_cfg >= 0 && ws->ov.gemm_cfg <= 3) return ws->ov.gemm_cfg == 3 && w->bits != 4 ? -1 : ws->ov.gemm_cfg;
     if (w->bits != 4) return -1;
     const GemmTileCfg big = gemm32_tile(w->bits, 1);
     const int cols = sw ? w->N / 2 : w->N, bcols = sw ? big.bn / 2 : big.bn;
     const int64_t big_tiles = (int64_t)((rows + big.bm - 1) / big.bm) * ((cols + bcols - 1) / bcols);
-    return big_tiles >= 4 * ws->cu_count ? 1 : -1;
+    if (big_tiles >= 4 * ws->cu_count) return 1;
+    // A SiLU-gate GEMM whose 256 x 192 grid covers 3/4 to all of the CUs once (gate_up at
+    // 512 tokens: 204 tiles) takes those tiles: twelve waves of 64 x 64 per CU do about 1.4x
+    // the work per CU of two 128 x 128 tiles of the 16x16x64 kernel, whose 608 tiles would
+    // leave a short second round (M = 512 gate_up 39.8 -> 35.2 us).
+    if (sw) {
+        const GemmTileCfg t3 = gemm32_tile(4, 3);
+        const int64_t tiles3 = (int64_t)((rows + t3.bm - 1) / t3.bm) * ((cols + t3.bn / 2 - 1) / (t3.bn / 2));
+        if (tiles3 <= ws->cu_count && 4 * tiles3 >= 3 * (int64_t)ws->cu_count) return 3;
+    }
+    return -1;
 }
 
 int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_t flags, GemmPlan* out) {

@@ -55,6 +55,7 @@ namespace g32 {
 
 constexpr int BK = 128;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 word 3)
+constexpr int kPastEnd = 0x7fff0000;      // a buffer offset past every operand (reads return zeros)
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -69,12 +70,18 @@ struct Geom {
     static constexpr int STAGE = A_BYTES + B_BYTES;
     static constexpr int LDS = NST * STAGE;
     static constexpr int A_BLK_ROWS = 1024 / A_ROW, B_BLK_ROWS = 1024 / B_ROW;  // rows per 1 KiB copy
-    static constexpr int NA = A_BYTES / 1024 / NW, NBC = B_BYTES / 1024 / NW;  // copies per wave per stage
+    static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
+    // copies per wave per stage; when the blocks do not divide among the waves, the last
+    // slots read past their buffer (no memory access) into a scratch KiB after the stages,
+    // so every wave issues the same number of copies and the copy waits stay uniform
+    static constexpr int NA = (A_BLOCKS + NW - 1) / NW, NBC = (B_BLOCKS + NW - 1) / NW;
+    static constexpr bool SPARE = NA * NW > A_BLOCKS || NBC * NW > B_BLOCKS;
+    static constexpr int SCRATCH = NST * STAGE;  // byte offset of the scratch KiB
     static constexpr int NL = NA + NBC;
-    static constexpr int LDS_ALL = NST * STAGE;
+    static constexpr int LDS_ALL = NST * STAGE + (SPARE ? 1024 : 0);
     static constexpr int REGS = MB * NB * 16;  // int32 accumulators per lane
     static_assert(MB >= 1 && NB >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tile");
-    static_assert(NA >= 1 && NBC >= 1 && NA * NW * 1024 == A_BYTES && NBC * NW * 1024 == B_BYTES, "copy plan");
+    static_assert(NA >= 1 && NBC >= 1 && A_BLOCKS * 1024 == A_BYTES && B_BLOCKS * 1024 == B_BYTES, "copy plan");
     static_assert(LDS_ALL <= 160 * 1024 && NST >= 3, "LDS stages");
 };
 
@@ -160,7 +167,7 @@ struct Copy {
 #pragma unroll
         for (int i = 0; i < G::NA; ++i) {
             const int row = (wave * G::NA + i) * 8 + (lane >> 3);
-            aoff[i] = row * (int)p.ldq + (((lane & 7) ^ swz128(row)) << 4);
+            aoff[i] = row * (int)p.ldq + (((lane & 7) ^ swz128(row)) << 4);  // a spare slot: row >= BM, past ra
         }
 #pragma unroll
         for (int i = 0; i < G::NBC; ++i) {
@@ -174,7 +181,7 @@ struct Copy {
                 chunk = (lane & 3) ^ swz64(row);
             }
             if (SWIGLU && row >= BN / 2) row -= BN / 2;
-            boff[i] = row * (int)p.wrow + (chunk << 4);
+            boff[i] = blk < G::B_BLOCKS ? row * (int)p.wrow + (chunk << 4) : kPastEnd;
         }
     }
 
@@ -182,12 +189,17 @@ struct Copy {
     __device__ __forceinline__ void issue(uint8_t* smem, int stage, int kt) const {
         const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < G::NA; ++i) dma16(ra, smem + stage + (wave * G::NA + i) * 1024, aoff[i], k0);
+        for (int i = 0; i < G::NA; ++i) {
+            const int blk = wave * G::NA + i;  // wave-uniform
+            uint8_t* dst = G::SPARE && blk >= G::A_BLOCKS ? smem + G::SCRATCH : smem + stage + blk * 1024;
+            dma16(ra, dst, aoff[i], k0);
+        }
 #pragma unroll
         for (int i = 0; i < G::NBC; ++i) {
             const int blk = wave * G::NBC + i;
             const bool up = SWIGLU && blk * G::B_BLK_ROWS >= BN / 2;
-            dma16(up ? ru : rg, smem + stage + G::A_BYTES + blk * 1024, boff[i], BITS == 8 ? k0 : k0 / 2);
+            uint8_t* dst = G::SPARE && blk >= G::B_BLOCKS ? smem + G::SCRATCH : smem + stage + G::A_BYTES + blk * 1024;
+            dma16(up ? ru : rg, dst, boff[i], BITS == 8 ? k0 : k0 / 2);
         }
     }
 
@@ -473,6 +485,8 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
 //         when the grid holds at most one workgroup per CU
 //   W4 1: 256 x 256, 2 x 4 waves of 128 x 64, 3 x 48 KiB
 //   W4 2: 128 x 256, 2 x 4 waves of 64 x 64, 4 x 32 KiB
+//   W4 3: 256 x 192, 4 x 3 waves of 64 x 64, 3 x 44 KiB (gate_up at 512 tokens: 204 tiles,
+//         about one per CU; twelve waves keep the four SIMDs evenly loaded)
 //   W8 0: 128 x 128, 2 x 2 waves of 64 x 64, 3 x 32 KiB, or 4 when at most one per CU
 //   W8 1: 256 x 128, 2 x 2 waves of 128 x 64, 3 x 48 KiB
 //   W8 2: 128 x 256, 2 x 4 waves of 64 x 64, 3 x 48 KiB
@@ -480,6 +494,7 @@ GemmTileCfg gemm32_tile(int bits, int cfg) {
     switch (cfg) {
         case 1: return bits == 4 ? GemmTileCfg{256, 256, 512, 128} : GemmTileCfg{256, 128, 256, 128};
         case 2: return GemmTileCfg{128, 256, 512, 64};
+        case 3: return GemmTileCfg{256, 192, 768, 64};
         default: return GemmTileCfg{128, 128, 256, 64};
     }
 }
@@ -491,6 +506,7 @@ hipError_t launch_gemm32(const GemmParams& p, int bits, int cfg, hipStream_t st)
                                   : g32::launch_cfg<4, 128, 128, 2, 2, 3>(p, st);
             case 1: return g32::launch_cfg<4, 256, 256, 2, 4, 3>(p, st);
             case 2: return g32::launch_cfg<4, 128, 256, 2, 4, 4>(p, st);
+            case 3: return g32::launch_cfg<4, 256, 192, 4, 3, 3>(p, st);
         }
     } else {
         switch (cfg) {

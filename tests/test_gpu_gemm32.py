@@ -1,9 +1,10 @@
 """The 32x32x32 MFMA GEMM in each of its tile configurations, forced through QLIN_GEMM_CFG
 (a workspace reads the override when it is created), against the oracle: int32 sums
 bit-exact, plain fp16 outputs bit-exact, SiLU-gate within 1e-3, the residual update
-bit-exact; ragged M and N, split K, W4 and W8.  By default the library takes this kernel
-only for large grids (e.g. the M = 4096 gate_up), so these tests keep every configuration
-covered."""
+bit-exact; ragged M and N, split K, W4 and W8 (configuration 3 is W4 only).  By default the
+library takes this kernel only for large grids (e.g. the M = 4096 gate_up) and for the
+SiLU-gate GEMM whose 256 x 192 grid covers the CUs about once (the M = 512 gate_up), so these
+tests keep every configuration covered."""
 import os
 
 import numpy as np
@@ -30,10 +31,12 @@ def cfg_ws(cfg, rows, K, N, splits=None):
         os.environ.pop("QLIN_GEMM_SPLITS", None)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("K,N,M,splits", [(2560, 1024, 300, None), (4096, 640, 17, 3), (1024, 2000, 513, 2)])
 def test_gemm32_configs_match_oracle(oracle, cfg, bits, K, N, M, splits):
+    if cfg == 3 and bits == 8:
+        pytest.skip("configuration 3 is W4 only")
     codes = synth.codes(N, K, bits, 600 + cfg + K % 7 + bits).numpy()
     sc = synth.scales(N, bits, 601 + bits).numpy()
     w = make_weights(bits, codes, sc)
@@ -88,6 +91,35 @@ def test_gemm32_is_default_for_large_grids():
     ref = ql.run(ws16, w, A, flags=ql.QLIN_SWIGLU)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    ws.close()
+    ws16.close()
+    w.close()
+
+
+def test_gemm32_gate_up_512_takes_256x192():
+    """The M = 512 gate_up (W4, SiLU-gate) takes the 256 x 192 tiles by default (204 tiles for
+    256 CUs), and its output equals the 16x16x64 kernel's bit for bit; so do a ragged M = 500
+    and, with the tiles forced, the residual-free plain output of the same weights."""
+    name, K, N = synth.LAYER[2]
+    packed, codes, sc = synth.make_linear(N, K, 4, synth.linear_seed(0, 2), device=DEV)
+    w = ql.Weights.from_packed_device(4, K, N, packed, sc)
+    ws = ql.Workspace(512, K, N)
+    os.environ["QLIN_GEMM_KERNEL"] = "16"
+    try:
+        ws16 = ql.Workspace(512, K, N)
+    finally:
+        del os.environ["QLIN_GEMM_KERNEL"]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for M in (512, 500):
+        A = synth.activations(M, K, seed=611 + M, device=DEV)
+        pl = ql.plan(ws, w, A, ql.QLIN_SWIGLU)
+        if cus == 256:
+            assert pl["tile_m"] == 256 and pl["tile_n"] == 96 and pl["splits"] == 1, pl
+        assert ql.plan(ws16, w, A, ql.QLIN_SWIGLU)["tile_m"] == 128
+        out = ql.run(ws, w, A, flags=ql.QLIN_SWIGLU)
+        ref = ql.run(ws16, w, A, flags=ql.QLIN_SWIGLU)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), M
     ws.close()
     ws16.close()
     w.close()
