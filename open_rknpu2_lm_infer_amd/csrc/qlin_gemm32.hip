@@ -68,7 +68,6 @@ struct Geom {
     static constexpr int A_ROW = BK, B_ROW = BITS == 4 ? BK / 2 : BK;
     static constexpr int A_BYTES = BM * A_ROW, B_BYTES = BN * B_ROW;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS = NST * STAGE;
     static constexpr int A_BLK_ROWS = 1024 / A_ROW, B_BLK_ROWS = 1024 / B_ROW;  // rows per 1 KiB copy
     static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
     // copies per wave per stage; when the blocks do not divide among the waves, the last
