@@ -306,6 +306,7 @@ static bool launch_quant_reg_w(const QuantParams& p, int rows, hipStream_t strea
     dim3 grid((rows + 4 / WPR - 1) / (4 / WPR)), block(256);
     if (per_lane <= 2) quant_rows_reg_kernel<T, 2, WPR><<<grid, block, 0, stream>>>(p, rows);
     else if (per_lane <= 4) quant_rows_reg_kernel<T, 4, WPR><<<grid, block, 0, stream>>>(p, rows);
+    else if (per_lane <= 6) quant_rows_reg_kernel<T, 6, WPR><<<grid, block, 0, stream>>>(p, rows);  // K = 9728
     else if (per_lane <= 8) quant_rows_reg_kernel<T, 8, WPR><<<grid, block, 0, stream>>>(p, rows);
     else if (per_lane <= 12) quant_rows_reg_kernel<T, 12, WPR><<<grid, block, 0, stream>>>(p, rows);
     else if (per_lane <= 20) quant_rows_reg_kernel<T, 20, WPR><<<grid, block, 0, stream>>>(p, rows);
