@@ -696,8 +696,9 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
         // tiles per split, and take the count with the least estimated time: a split's
         // longest k range at ~0.45 us per k tile, plus for a split tile ~1.5 us of round
         // trips and its partials (written by every split, read by the last) at ~4.5 TB/s.
-        // Measured at M = 512: o (K = 4096, 80 tiles) 18.2 us with 2 splits, 18.9 with 3;
-        // down (K = 9728) 26.8 / 24.7 us.  Filling the CUs alone took 3 for both.
+        // Measured at M = 512: o (K = 4096, 80 tiles) 18.2 us with 2 splits, 18.9 with 3,
+        // 19.4 unsplit; down (K = 9728) 26.8 / 24.7 us, 38.4 unsplit.  Filling the CUs alone
+        // took 3 for both.
         const int target = ov.gemm_target_wgs > 0 ? ov.gemm_target_wgs : ws->cu_count;
         const int smax = std::max(1, std::min((target + tiles / 2) / tiles, ktiles / 4));
         S = 1;
