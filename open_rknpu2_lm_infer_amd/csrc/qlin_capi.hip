@@ -695,17 +695,21 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
         // trip costs more than a second resident workgroup per CU gains), keeping >= 4 k
         // tiles per split, and take the count with the least estimated time: a split's
         // longest k range at ~0.45 us per k tile, plus for a split tile ~1.5 us of round
-        // trips and its partials (written by every split, read by the last) at ~4.5 TB/s.
-        // Measured at M = 512: o (K = 4096, 80 tiles) 18.2 us with 2 splits, 18.9 with 3,
-        // 19.4 unsplit; down (K = 9728) 26.8 / 24.7 us, 38.4 unsplit.  Filling the CUs alone
-        // took 3 for both.
+        // trips and its partials (written by every split, read by the last) at ~4.5 TB/s,
+        // or ~9 TB/s when the tile count is a multiple of 8: then the XCD-contiguous order
+        // puts all splits of a tile on one XCD.  Measured at M = 512 (80 tiles): o (K =
+        // 4096) 15.2 us with 3 splits, 15.9 with 2; down (K = 9728) 23.8 / 26.1 us; 4
+        // splits (more workgroups than CUs) 20.7 / 29.4.  With the splits of a tile on
+        // different XCDs, o took 18.2 us with 2 splits, 18.9 with 3, and unsplit o / down
+        // took 19.4 / 38.4 us.
         const int target = ov.gemm_target_wgs > 0 ? ov.gemm_target_wgs : ws->cu_count;
         const int smax = std::max(1, std::min((target + tiles / 2) / tiles, ktiles / 4));
+        const double part_rate = tiles % 8 == 0 ? 9.0e6 : 4.5e6;  // partial bytes per us
         S = 1;
         double best = 1e30;
         for (int t = 1; t <= smax; ++t) {
             const int per = ((ktiles + t - 1) / t + 1) & ~1;  // even k tiles per split
-            const double exch = t > 1 ? 1.5 + (2.0 * t - 1) * tiles * slice * 4.0 / 4.5e6 : 0.0;
+            const double exch = t > 1 ? 1.5 + (2.0 * t - 1) * tiles * slice * 4.0 / part_rate : 0.0;
             const double est = 0.45 * per + exch;
             if (est < best - 1e-9) {
                 best = est;

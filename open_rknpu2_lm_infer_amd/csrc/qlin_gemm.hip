@@ -39,6 +39,9 @@
 // Split-K: `splits` workgroups share a tile; each writes its int32 partial
 // thread-major with device-coherent stores, waits for them, bumps the tile counter,
 // and the last one sums the others, runs the epilogue and re-zeroes the counter.
+// The splits of a tile are adjacent in the XCD-contiguous workgroup order, so when
+// the grid divides among the 8 XCDs they run on one XCD (M = 512 o, 80 tiles x 2
+// splits: 16.0 us against 17.8 with the splits of a tile on different XCDs).
 #include <hip/hip_fp16.h>
 
 #include "qlin_internal.hpp"
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(128 * WN) void gemm_kernel(GemmParams p) {
     const int NG = tiles * p.splits;
     int b = blockIdx.x;
     if ((NG & 7) == 0) b = (b & 7) * (NG >> 3) + (b >> 3);  // contiguous tile ranges per XCD
-    const int z = b / tiles, tile = b - z * tiles;
+    const int z = b % p.splits, tile = b / p.splits;  // the splits of a tile adjacent
     // groups of group_m m-tiles sweep all n tiles, m fastest: the workgroups resident on
     // one XCD share a few A row blocks and B column blocks in its L2
     const int per_group = p.group_m * p.n_tiles;

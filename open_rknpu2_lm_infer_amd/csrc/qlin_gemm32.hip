@@ -45,6 +45,8 @@
 // Split-K: `splits` workgroups share a tile; each writes its int32 partial thread-major
 // with device-coherent stores, waits for them, bumps the tile counter, and the last one
 // sums the others, runs the epilogue and re-zeroes the counter (no memset in a graph).
+// The splits of a tile are adjacent in the XCD-contiguous workgroup order, as in
+// gemm_kernel.
 #include <hip/hip_fp16.h>
 
 #include "qlin_internal.hpp"
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm32_kernel(GemmParams p) {
     const int NG = tiles * p.splits;
     int b = blockIdx.x;
     if ((NG & 7) == 0) b = (b & 7) * (NG >> 3) + (b >> 3);  // contiguous tile ranges per XCD
-    const int z = b / tiles, tile = b - z * tiles;
+    const int z = b % p.splits, tile = b / p.splits;  // the splits of a tile adjacent
     const int per_group = p.group_m * p.n_tiles;
     const int g = tile / per_group, first_m = g * p.group_m;
     const int gm = min(p.m_tiles - first_m, p.group_m);
