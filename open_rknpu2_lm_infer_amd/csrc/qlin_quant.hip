@@ -85,7 +85,8 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(QuantParams p) 
 // waves (the least latency per row); with many rows, 64 (one wave per row, many rows
 // resident per CU) keeps more rows' sequential norm chains in flight at once, where
 // 256-thread rows left three of four waves idle during the sum (M = 4096, K = 2560 with
-// RMSNorm: 19.6 -> 14.6 us).  Rows of up to kStageBytes take this path (the
+// RMSNorm: 19.6 -> 14.6 us).  Many RMSNorm rows of up to 8 chunks per lane with 16-byte
+// aligned weights take quant_norm_wave_kernel instead.  Rows of up to kStageBytes take this path (the
 // default 64 KiB workgroup LDS limit, less the static reduction words).  Needs
 // K % 8 == 0 and a 16-byte aligned row (16-byte copies).
 constexpr int kStageBytes = 60 * 1024;
@@ -198,6 +199,101 @@ __global__ __launch_bounds__(NT) void quant_rows_staged_kernel(QuantParams p) {
         p.s[row] = s;
         if (f && p.err) atomicOr(p.err, 1u);
     }
+}
+
+// RMSNorm rows, one wave per row, row and RMSNorm weights in registers: the lane's NC
+// 16-byte row chunks and their weights are all loaded before any is used, the row is
+// copied into LDS only for the norm sum (the reference's chain order reads it there),
+// and the normalized values stay in registers for the absmax and the quantize pass.
+// The staged kernel loads the weights again in both passes, a dependent global round
+// trip per 8 values (M = 4096, K = 2560: 17.5 us there).  Same arithmetic as the staged
+// kernel, value for value.  Needs K % 8 == 0, a 16-byte aligned row and weights, an
+// 8-byte aligned q with ldq % 8 == 0, and 64 * NC chunks >= K / E.
+template <typename T, int NC>
+__global__ __launch_bounds__(64) void quant_norm_wave_kernel(QuantParams p) {
+    extern __shared__ __align__(16) uint8_t stage[];
+    constexpr int E = 16 / sizeof(T);  // values per 16-byte chunk
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const T* x = reinterpret_cast<const T*>(p.A) + (int64_t)row * p.lda;
+    T* xs = reinterpret_cast<T*>(stage);
+    const int nchunks = p.K / E;
+    // (a clamped chunk repeats the last one: harmless for the max and the finiteness test,
+    // and its LDS copy writes the same bytes to the same place)
+    uint4 raw[NC];
+    float v[NC][E];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) raw[i] = reinterpret_cast<const uint4*>(x)[min(lane + 64 * i, nchunks - 1)];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const float4* g = reinterpret_cast<const float4*>(p.gamma + (int64_t)min(lane + 64 * i, nchunks - 1) * E);
+#pragma unroll
+        for (int h = 0; h < E / 4; ++h) {
+            const float4 a = g[h];
+            v[i][4 * h] = a.x;
+            v[i][4 * h + 1] = a.y;
+            v[i][4 * h + 2] = a.z;
+            v[i][4 * h + 3] = a.w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) reinterpret_cast<uint4*>(xs)[min(lane + 64 * i, nchunks - 1)] = raw[i];
+    __syncthreads();
+    const float sum = (p.flags & kFlagNormSeq) ? (lane == 0 ? lds_sumsq_seq(xs, p.K) : 0.0f) : lds_sumsq_neon16(xs, p.K);
+    const float nscale = __shfl(1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps), 0, 64);
+
+    // normalized values (v: weight -> value), absmax (after the norm), finiteness (of the input)
+    float m = 0.0f;
+    int f = 0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const T* e = reinterpret_cast<const T*>(&raw[i]);
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const float xv = lds_ld(e, j);
+            f |= !__builtin_isfinite(xv);
+            v[i][j] = (xv * nscale) * v[i][j];
+            m = fmaxf(m, fabsf(v[i][j]));
+        }
+    }
+    m = wave_max(m);
+    f = wave_or(f);
+    const float s = qscale_from_absmax(m);
+    const float inv = 1.0f / s;
+    const bool rne = (p.flags & kFlagRne) != 0;
+    const bool fast = !f && __builtin_isfinite(s);  // finite row: the short rounding sequence
+    int8_t* qrow = p.q + (int64_t)row * p.ldq;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunks) {
+            if constexpr (E == 8) {
+                uint32_t w0, w1;
+                quant8(v[i], inv, rne, fast, w0, w1);
+                *reinterpret_cast<uint2*>(qrow + c * E) = make_uint2(w0, w1);
+            } else {
+                *reinterpret_cast<uint32_t*>(qrow + c * E) = quant4(v[i], inv, rne, fast);
+            }
+        }
+    }
+    for (int k0 = p.K + 8 * lane; k0 < p.ldq; k0 += 8 * 64) *reinterpret_cast<uint2*>(qrow + k0) = make_uint2(0, 0);
+    if (lane == 0) {
+        p.s[row] = s;
+        if (f && p.err) atomicOr(p.err, 1u);
+    }
+}
+
+template <typename T>
+static bool launch_quant_norm_wave(const QuantParams& p, int rows, hipStream_t stream) {
+    constexpr int E = 16 / sizeof(T);
+    const int per_lane = (p.K / E + 63) / 64;
+    const size_t row_bytes = (size_t)p.K * sizeof(T);
+    dim3 grid(rows), block(64);
+    if (per_lane <= 2) quant_norm_wave_kernel<T, 2><<<grid, block, row_bytes, stream>>>(p);
+    else if (per_lane <= 4) quant_norm_wave_kernel<T, 4><<<grid, block, row_bytes, stream>>>(p);
+    else if (per_lane <= 5) quant_norm_wave_kernel<T, 5><<<grid, block, row_bytes, stream>>>(p);  // K = 2560 fp16
+    else if (per_lane <= 8) quant_norm_wave_kernel<T, 8><<<grid, block, row_bytes, stream>>>(p);
+    else return false;
+    return true;
 }
 
 // Without RMSNorm: WPR waves per row (1 or 4) and 4 / WPR rows per 256-thread
@@ -335,6 +431,11 @@ hipError_t launch_quant(const QuantParams& p, int rows, hipStream_t stream) {
     if (vec && qvec && row_bytes <= (size_t)kStageBytes) {
         // many rows: one wave per row (see quant_rows_staged_kernel)
         const bool wave_rows = rows >= 1024;
+        if (wave_rows && p.gamma && (reinterpret_cast<uintptr_t>(p.gamma) & 15) == 0) {
+            const bool ok = p.a_f16 ? launch_quant_norm_wave<__half>(p, rows, stream)
+                                    : launch_quant_norm_wave<float>(p, rows, stream);
+            if (ok) return hipGetLastError();
+        }
         const dim3 sblock(wave_rows ? 64 : kRowThreads);
         if (p.a_f16) {
             if (wave_rows) quant_rows_staged_kernel<__half, 64><<<grid, sblock, row_bytes, stream>>>(p);
