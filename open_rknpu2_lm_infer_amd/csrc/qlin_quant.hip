@@ -209,7 +209,43 @@ __global__ __launch_bounds__(NT) void quant_rows_staged_kernel(QuantParams p) {
 // trip per 8 values (M = 4096, K = 2560: 17.5 us there).  Same arithmetic as the staged
 // kernel, value for value.  Needs K % 8 == 0, a 16-byte aligned row and weights, an
 // 8-byte aligned q with ldq % 8 == 0, and 64 * NC chunks >= K / E.
-template <typename T, int NC>
+// Sum of squares in the order of src/model/cpu.rs:14-35 (16 fused-multiply-add chains,
+// chain j takes elements j, j+16, ... in order, combined lanewise as (a+b)+(c+d), then
+// (t0+t1)+(t2+t3); K % 16 == 0 so there is no scalar tail), from a row stored
+// chain-major in LDS: element k at cm[(k % 16) * ls + k / 16], ls = K / 16 + 8.  Lane j
+// of the wave reads chain j 8 elements per 16-byte read (K / 128 reads instead of K / 16
+// two-byte reads; with 16 rows per CU the two-byte reads held the sum at ~3.6 us per row
+// against ~1.1 us alone).  The 8-element pad puts the 16 chains' reads, and the two
+// chains written by one store instruction, in different banks.  Needs K % 512 == 0
+// (trips of four reads).  Called by all 64 lanes; the result is valid in lane 0.
+__device__ __forceinline__ float cm_sumsq_neon16(const _Float16* cm, int K) {
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int ls = K / 16 + 8;
+    float acc = 0.0f;
+    if (lane < 16) {
+        const uint4* c = reinterpret_cast<const uint4*>(cm + j * ls);
+        for (int r = 0; r < K / 128; r += 4) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = c[r + u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const _Float16* h = reinterpret_cast<const _Float16*>(&v[u]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f = (float)h[e];
+                    acc = __builtin_fmaf(f, f, acc);
+                }
+            }
+        }
+    }
+    const float b = __shfl(acc, j + 4, 64), c = __shfl(acc, j + 8, 64), d = __shfl(acc, j + 12, 64);
+    const float tj = (acc + b) + (c + d);
+    const float t1 = __shfl(tj, 1, 64), t2 = __shfl(tj, 2, 64), t3 = __shfl(tj, 3, 64);
+    return (tj + t1) + (t2 + t3);
+}
+
+template <typename T, int NC, bool CM>
 __global__ __launch_bounds__(64) void quant_norm_wave_kernel(QuantParams p) {
     extern __shared__ __align__(16) uint8_t stage[];
     constexpr int E = 16 / sizeof(T);  // values per 16-byte chunk
@@ -235,10 +271,26 @@ __global__ __launch_bounds__(64) void quant_norm_wave_kernel(QuantParams p) {
             v[i][4 * h + 3] = a.w;
         }
     }
+    if constexpr (CM) {
+        // chain-major copy: chunk c holds elements 8c .. 8c + 7, i.e. chains 8 (c & 1) + e at
+        // position c >> 1
+        _Float16* cm = reinterpret_cast<_Float16*>(stage);
+        const int ls = p.K / 16 + 8;
 #pragma unroll
-    for (int i = 0; i < NC; ++i) reinterpret_cast<uint4*>(xs)[min(lane + 64 * i, nchunks - 1)] = raw[i];
+        for (int i = 0; i < NC; ++i) {
+            const int c = min(lane + 64 * i, nchunks - 1);
+            const _Float16* h = reinterpret_cast<const _Float16*>(&raw[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) cm[(8 * (c & 1) + e) * ls + (c >> 1)] = h[e];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) reinterpret_cast<uint4*>(xs)[min(lane + 64 * i, nchunks - 1)] = raw[i];
+    }
     __syncthreads();
-    const float sum = (p.flags & kFlagNormSeq) ? (lane == 0 ? lds_sumsq_seq(xs, p.K) : 0.0f) : lds_sumsq_neon16(xs, p.K);
+    float sum;
+    if constexpr (CM) sum = cm_sumsq_neon16(reinterpret_cast<const _Float16*>(stage), p.K);
+    else sum = (p.flags & kFlagNormSeq) ? (lane == 0 ? lds_sumsq_seq(xs, p.K) : 0.0f) : lds_sumsq_neon16(xs, p.K);
     const float nscale = __shfl(1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps), 0, 64);
 
     // normalized values (v: weight -> value), absmax (after the norm), finiteness (of the input)
@@ -282,18 +334,27 @@ __global__ __launch_bounds__(64) void quant_norm_wave_kernel(QuantParams p) {
     }
 }
 
-template <typename T>
-static bool launch_quant_norm_wave(const QuantParams& p, int rows, hipStream_t stream) {
+template <typename T, bool CM>
+static bool launch_quant_norm_wave_cm(const QuantParams& p, int rows, hipStream_t stream) {
     constexpr int E = 16 / sizeof(T);
     const int per_lane = (p.K / E + 63) / 64;
-    const size_t row_bytes = (size_t)p.K * sizeof(T);
+    const size_t lds = CM ? (size_t)(p.K + 128) * 2 : (size_t)p.K * sizeof(T);  // 16 chains of K / 16 + 8
     dim3 grid(rows), block(64);
-    if (per_lane <= 2) quant_norm_wave_kernel<T, 2><<<grid, block, row_bytes, stream>>>(p);
-    else if (per_lane <= 4) quant_norm_wave_kernel<T, 4><<<grid, block, row_bytes, stream>>>(p);
-    else if (per_lane <= 5) quant_norm_wave_kernel<T, 5><<<grid, block, row_bytes, stream>>>(p);  // K = 2560 fp16
-    else if (per_lane <= 8) quant_norm_wave_kernel<T, 8><<<grid, block, row_bytes, stream>>>(p);
+    if (per_lane <= 2) quant_norm_wave_kernel<T, 2, CM><<<grid, block, lds, stream>>>(p);
+    else if (per_lane <= 4) quant_norm_wave_kernel<T, 4, CM><<<grid, block, lds, stream>>>(p);
+    else if (per_lane <= 5) quant_norm_wave_kernel<T, 5, CM><<<grid, block, lds, stream>>>(p);  // K = 2560 fp16
+    else if (per_lane <= 8) quant_norm_wave_kernel<T, 8, CM><<<grid, block, lds, stream>>>(p);
     else return false;
     return true;
+}
+
+// fp16 rows in the reference's chain order with K % 512 == 0 take the chain-major sum
+template <typename T>
+static bool launch_quant_norm_wave(const QuantParams& p, int rows, hipStream_t stream) {
+    if constexpr (sizeof(T) == 2) {
+        if (!(p.flags & kFlagNormSeq) && p.K % 512 == 0) return launch_quant_norm_wave_cm<T, true>(p, rows, stream);
+    }
+    return launch_quant_norm_wave_cm<T, false>(p, rows, stream);
 }
 
 // Without RMSNorm: WPR waves per row (1 or 4) and 4 / WPR rows per 256-thread
