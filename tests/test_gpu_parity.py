@@ -112,7 +112,9 @@ def test_rmsnorm_quantize_bitexact(oracle, order, M, K):
 @pytest.mark.parametrize("order", ["neon16", "seq"])
 @pytest.mark.parametrize("M,K", [(1027, 2560), (1030, 104), (1025, 9728)])
 def test_rmsnorm_quantize_many_rows(oracle, dtype, order, M, K):
-    """Many rows take the one-wave-per-row staged kernel (64-thread workgroups)."""
+    """Many rows take one wave per row: rows and RMSNorm weights in registers (fp16 rows up to
+    K = 4096, the chain-major sum for K % 512 == 0 in the chain order; f32 rows up to K = 2048),
+    else the staged kernel (64-thread workgroups)."""
     x = synth.activations(M, K, seed=K + M, device="cpu", dist="student_t3").to(dtype)
     gam = synth.gamma(K, seed=K, device="cpu")
     flags = ql.QLIN_NORM_SEQUENTIAL if order == "seq" else 0
@@ -125,6 +127,34 @@ def test_rmsnorm_quantize_many_rows(oracle, dtype, order, M, K):
     qh = q.cpu().numpy()
     assert np.array_equal(qh[:, :K], qo)
     assert not qh[:, K:].any()  # the zero tail up to ldq
+
+
+@pytest.mark.parametrize("dtype,K", [(torch.float16, 2560), (torch.float16, 104), (torch.float32, 2560)])
+def test_rmsnorm_quantize_many_rows_nonfinite(oracle, dtype, K):
+    """Rows holding NaN, Inf or -Inf among 1030 RMSNorm rows (fp16 K = 2560: the chain-major
+    sum; K = 104: the row-major sum; f32 K = 2560: the staged kernel): the error word is set,
+    the oracle counts three bad rows, every row's codes equal the oracle's and the finite rows'
+    scales do too."""
+    M = 1030
+    x = synth.activations(M, K, seed=K + 7, device="cpu", dist="student_t3").to(dtype)
+    x[3, 5] = float("nan")
+    x[700, K - 1] = float("inf")
+    x[M - 1, 0] = float("-inf")
+    gam = synth.gamma(K, seed=K, device="cpu")
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ldq = roundup(K, 256)
+    q, s = ql.quantize(x.to(DEV), ldq=ldq, gamma=gam.to(DEV), eps=1e-6, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    y = oracle.rmsnorm(x.float().numpy(), gam.numpy(), 1e-6, "neon16")
+    qo, so, bad = oracle.quantize(y)
+    assert bad == 3
+    qh = q.cpu().numpy()
+    assert np.array_equal(qh[:, :K], qo)
+    assert not qh[:, K:].any()
+    finite = np.ones(M, dtype=bool)
+    finite[[3, 700, M - 1]] = False
+    assert np.array_equal(s.cpu().numpy().view(np.uint32)[finite], so.view(np.uint32)[finite])
 
 
 # ------------------------------------------------------------------ integer accumulators
