@@ -311,6 +311,30 @@ def test_nonfinite_activation_sets_status(ws):
     w.close()
 
 
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("M", [1, 4, 40, 1030])
+def test_nonfinite_row_sets_status_every_path(ws, M, norm):
+    """One Inf in the last activation row sets the sticky error word on every path: the
+    fused-quantization GEMV (1 and 4 rows), the quantize launch before the GEMM (40 rows) and
+    the many-rows quantize kernels (1030 rows), with and without RMSNorm; a clean run after it
+    leaves the word clear."""
+    K, N = 2560, 256
+    codes = synth.codes(N, K, 4, 3).numpy()
+    w = make_weights(4, codes, synth.scales(N, 4, 4).numpy())
+    g = synth.gamma(K, seed=3, device=DEV) if norm else None
+    A = synth.activations(M, K, seed=M, device=DEV)
+    ws.status(clear=True)
+    ql.run(ws, w, A, gamma=g, eps=1e-6)
+    assert ws.status(clear=True) == 0
+    bad = A.clone()
+    bad[M - 1, 17] = float("inf")
+    ql.run(ws, w, bad, gamma=g, eps=1e-6)
+    assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
+    ql.run(ws, w, A, gamma=g, eps=1e-6)
+    assert ws.status(clear=True) == 0
+    w.close()
+
+
 # ------------------------------------------------------------------ reference test cases
 
 
