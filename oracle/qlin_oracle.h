@@ -28,7 +28,8 @@ extern "C" {
 #endif
 
 /* rounding of x*(1/s): 0 = half away from zero (Rust f32::round, the reference
- * default, src/npu.rs:1109), 1 = half to even (BASELINE config text). */
+ * default, src/npu.rs:1109), 1 = half to even (the rounding the W8A8 decode-GEMV
+ * workload description names; the library's QLIN_ROUND_HALF_EVEN). */
 #define ORACLE_ROUND_AWAY 0
 #define ORACLE_ROUND_EVEN 1
 
