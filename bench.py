@@ -67,6 +67,128 @@ def pct(xs, q):
     return xs[lo] + (xs[hi] - xs[lo]) * (i - lo)
 
 
+def calibrate(info):
+    """Hardware figures behind the roofline analysis, from the calibration kernels of
+    libqlcalib.so and the library's own GEMV at a tiny width; each timed with HIP events
+    over a graph of back-to-back launches."""
+    import ctypes
+
+    import torch
+
+    from open_rknpu2_lm_infer_amd import _lib
+    from open_rknpu2_lm_infer_amd import qlinear as ql
+    from open_rknpu2_lm_infer_amd import synth
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    cal = ctypes.CDLL(os.path.join(here, "open_rknpu2_lm_infer_amd", "libqlcalib.so"))
+    P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    cal.qcal_empty.argtypes = [I, I, P]
+    cal.qcal_stream.argtypes = [P, I64, I, P, P]
+    cal.qcal_mfma.argtypes = [I, I, P, P]
+    cal.qcal_lds_copy.argtypes = [P, I, I, P, P]
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def sp():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def per_call_us(fn, count, reps=10):
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(count):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * count)
+
+    sclk_ghz = info.sclk_khz / 1e6
+    cus = info.cu_count
+    out = {"cus": cus, "sclk_mhz_reported": info.sclk_khz / 1e3}
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    # 1. one empty launch in a graph
+    out["empty_launch_us"] = {
+        "1x64": round(per_call_us(lambda i: cal.qcal_empty(1, 64, sp()), 200), 3),
+        f"{cus}x512": round(per_call_us(lambda i: cal.qcal_empty(cus, 512, sp()), 200), 3),
+    }
+    log(f"calib: empty launch {out['empty_launch_us']}")
+    # 2. streaming floor: each launch reads a different slice of a 2 GiB buffer (no cache reuse)
+    big = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    sizes = {n: N * K // 2 + N * 4 for n, K, N in synth.LAYER}
+    sizes["sustained_1GiB"] = 1 << 30
+    stream = {}
+    for name, nb in sizes.items():
+        nb = (nb + 4095) // 4096 * 4096
+        slots = max(1, (big.numel() - nb) // nb)
+        us = per_call_us(lambda i, nb=nb, slots=slots: cal.qcal_stream(big.data_ptr() + (i % slots) * nb, nb, cus,
+                                                                        sink.data_ptr(), sp()),
+                         36 if nb < (1 << 30) else 4)
+        stream[name] = {"bytes": nb, "us": round(us, 3), "gbs": round(nb / (us * 1e-6) / 1e9, 1)}
+    out["stream_floor"] = stream
+    log(f"calib: stream floor {stream}")
+    del big
+    # 3. int8 matrix-core rate: 4 workgroups of 4 waves per CU, 4 independent MFMA chains per wave
+    iters, grid = 20000, 4 * cus
+    us = per_call_us(lambda i: cal.qcal_mfma(grid, iters, sink.data_ptr(), sp()), 4, 3)
+    ops = grid * 4 * iters * 4 * 32768.0
+    out["mfma_i8_16x16x64"] = {"tops": round(ops / (us * 1e-6) / 1e12, 1), "us": round(us, 1),
+                               "ops_per_cu_clk_at_reported_sclk": round(ops / (us * 1e-6) / cus / (sclk_ghz * 1e9), 1)}
+    log(f"calib: MFMA {out['mfma_i8_16x16x64']}")
+    # 4. global -> LDS copies of an L2-resident 64 KiB block, one and two workgroups per CU
+    src = torch.ones(64 * 1024, dtype=torch.uint8, device=dev)
+    cp = {}
+    for per_cu in (1, 2):
+        g_ = per_cu * cus
+        it = 2000
+        us = per_call_us(lambda i, g_=g_: cal.qcal_lds_copy(src.data_ptr(), g_, it, sink.data_ptr(), sp()), 4, 3)
+        b = g_ * 65536.0 * it
+        cp[f"{per_cu}_per_cu"] = {"tbs": round(b / (us * 1e-6) / 1e12, 2),
+                                  "bytes_per_cu_clk_at_reported_sclk": round(b / (us * 1e-6) / cus / (sclk_ghz * 1e9), 1)}
+    out["l2_to_lds_copy"] = cp
+    log(f"calib: L2 -> LDS copies {cp}")
+    # 5. the library's decode GEMV at a tiny width (K = 2560, N = 16 and 256; four weight sets):
+    #    launch, activation row, prologue and epilogue with next to no weight stream
+    ws = ql.Workspace(1, 2560, 2560)
+    x = synth.activations(1, 2560, seed=5, device=dev)
+    floor = {}
+    for N in (16, 256):
+        w = [ql.Weights.from_packed_device(4, 2560, N, *synth.make_linear(N, 2560, 4, 900 + j, device=dev)[::2])
+             for j in range(4)]
+        y = torch.empty((1, N), dtype=torch.float16, device=dev)
+        floor[f"W4 2560x{N}"] = round(per_call_us(lambda i, w=w, y=y: ql.run(ws, w[i % 4], x, out=y), 144), 3)
+        for ww in w:
+            ww.close()
+    ws.close()
+    out["gemv_floor_us"] = floor
+    log(f"calib: GEMV floor {floor}")
+    # 6. the platform BLAS: torch._int_mm (hipBLASLt, int8 x int8 -> int32, no quantization or epilogue)
+    blas = {}
+    try:
+        for M in (512, 4096):
+            tot_ops, tot_us = 0.0, 0.0
+            for name, K, N in synth.LAYER:
+                a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+                b = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev).t()
+                us = per_call_us(lambda i, a=a, b=b: torch._int_mm(a, b), 8, 5)
+                tot_ops += 2.0 * M * N * K
+                tot_us += us
+                blas[f"M{M}_{name}_us"] = round(us, 2)
+            blas[f"M{M}_tops"] = round(tot_ops / (tot_us * 1e-6) / 1e12, 1)
+    except Exception as ex:  # noqa: BLE001
+        blas["error"] = str(ex)[:200]
+    out["hipblaslt_int_mm"] = blas
+    log(f"calib: hipBLASLt {blas}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,7 +200,7 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "kernel", "gemm", "copy"], default="full")
+    ap.add_argument("--mode", choices=["full", "kernel", "gemm", "copy", "calib"], default="full")
     ap.add_argument("--stack-reps", type=int, default=5)
     ap.add_argument("--long-reps", type=int, default=3)
     ap.add_argument("--no-stack", action="store_true")
@@ -114,6 +236,9 @@ def main():
         return
     info = _lib.device_info(0)
     log(f"device: {torch.cuda.get_device_name(0)} CUs={info.cu_count} sclk={info.sclk_khz / 1e3:.0f} MHz")
+    if args.mode == "calib":
+        print(json.dumps(calibrate(info)), flush=True)
+        return
 
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

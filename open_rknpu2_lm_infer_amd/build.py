@@ -1,6 +1,7 @@
 """Builds libqlinear.so and libqlinear.a (the HIP kernels, the C ABI and the C++ npu
-mirror) in-tree for gfx950, and the native test binaries under tests/cpp/_build: the
-npu mirror's test and a C program linked against the static archive.
+mirror) in-tree for gfx950, libqlcalib.so (the calibration kernels of bench.py --mode
+calib, not part of the library), and the native test binaries under tests/cpp/_build:
+the npu mirror's test and a C program linked against the static archive.
 
     python -m open_rknpu2_lm_infer_amd.build
 
@@ -88,8 +89,23 @@ def build(verbose: bool = False) -> str:
         os.remove(tmp)
     subprocess.run(["ar", "rcs", tmp, *objs], check=True)
     os.replace(tmp, STATIC_LIB)
+    build_calib()
     build_tests()
     return LIB
+
+
+CALIB_SRC = os.path.join(HERE, "calib", "qlin_calib.hip")
+CALIB_LIB = os.path.join(HERE, "libqlcalib.so")
+
+
+def build_calib() -> str:
+    """Calibration kernels of the roofline figures (bench.py --mode calib); not part of
+    libqlinear.so."""
+    tmp = CALIB_LIB + ".tmp"
+    subprocess.run([HIPCC, *COMMON, "-shared", CALIB_SRC, "-o", tmp, "-Wl,-rpath,/opt/rocm/lib"], check=True,
+                   stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+    os.replace(tmp, CALIB_LIB)
+    return CALIB_LIB
 
 
 def build_tests() -> str:
@@ -100,11 +116,14 @@ def build_tests() -> str:
                     os.path.join(ROOT, "oracle", "qlin_oracle.c"), "-o", oracle_obj], check=True)
     subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", TEST_SRC, oracle_obj, "-o", TEST_BIN,
                     f"-L{HERE}", "-lqlinear", "-Wl,-rpath,$ORIGIN/../../../open_rknpu2_lm_infer_amd", "-lm"], check=True)
-    # a C caller of the static archive, linked as a Rust build.rs would link it
+    # a C caller of the static archive, linked as a Rust build.rs would link it (its GPU
+    # mode checks the kernels against the oracle, compiled in as the checker)
     static_obj = os.path.join(TEST_BUILD, "static_link_test.o")
-    subprocess.run(["gcc", "-O2", "-std=c11", "-Wall", "-c", STATIC_TEST_SRC, "-o", static_obj], check=True)
-    subprocess.run(["g++", static_obj, "-o", STATIC_TEST_BIN, "-Wl,--whole-archive", STATIC_LIB,
-                    "-Wl,--no-whole-archive", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"], check=True)
+    subprocess.run(["gcc", "-O2", "-std=c11", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-c",
+                    STATIC_TEST_SRC, "-o", static_obj], check=True)
+    subprocess.run(["g++", static_obj, oracle_obj, "-o", STATIC_TEST_BIN, "-Wl,--whole-archive", STATIC_LIB,
+                    "-Wl,--no-whole-archive", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib", "-lm"],
+                   check=True)
     return TEST_BIN
 
 

@@ -1160,11 +1160,6 @@ int qlin_chain_create(const qlin_chain_stage* st, int32_t n, int32_t max_rows, q
         cs.ncols = c->cols[s];
         chain_items(cs.ncols, c->grid, &cs.iw, &cs.ipw);
         cs.steps = w->Kp / (w->bits == 4 ? 256 : 128);
-        // a workgroup's share of the stage must fit the compute waves' registers at once
-        if (((d.flags & QLIN_SWIGLU) ? 2 : 1) * cs.ipw * cs.steps > chain_round_capacity()) {
-            rc = QLIN_ERR_UNSUPPORTED;
-            break;
-        }
         cs.gamma = d.gamma;
         cs.eps = d.eps;
         cs.x_offset = d.input == -1 ? d.input_offset : 0;

@@ -77,8 +77,6 @@ __device__ __forceinline__ ChainStage c_desc(const ChainParams& p, int s) {
 #endif
 }
 
-int chain_round_capacity() { return kCW * kCMaxE; }
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t c_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
 }
@@ -131,16 +129,6 @@ __device__ __forceinline__ void c_load(v4i (&buf)[kNB], const ChainStage& st, in
             ++ri;
         }
     }
-}
-
-// Weight steps E0 .. E1 - 1 of this wave's share of stage s.
-template <int E0, int E1>
-__device__ __forceinline__ void c_load_stage(const ChainParams& p, int s, v4i (&buf)[kNB]) {
-    const ChainStage st = c_desc(p, s);
-    const int wave = c_wave(), b = blockIdx.x;
-    const int E = c_row_items(st, c_items(st, b)) * st.steps;
-    const int f0 = E * wave / kCW, f1 = E * (wave + 1) / kCW;
-    c_load<E0, E1>(buf, st, b, f0, f1 - f0);
 }
 
 // Sums of one row item into LDS: lanes 0..15 hold channel `lane`, rows 0..3 in acc[0..3].
@@ -552,30 +540,35 @@ __device__ __forceinline__ void c_stage_helpers(const ChainParams& p, int s, uin
     }
 }
 
-// A compute wave's part of stage s.
+// A compute wave's part of stage s.  Its weight loads wait until the stage's input rows
+// are in LDS: loads in flight during the exchange sit ahead of the exchange's own loads
+// and stores in this CU's memory pipeline (issued right after the previous stage's
+// products, or half of them then, the 36-layer stack ran 1.2x / 1.13x slower).  A share
+// longer than the registers hold (e.g. a W8 SiLU-gate stage: K = 2560, N = 19456 is 120
+// steps per CU) runs in rounds of kCMaxE steps, each loaded once the previous round's
+// products are done.  The loads have one site in the code, so the weight registers have
+// a single owner (a second site made the compiler spill them).
 template <int MR>
 __device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i (&buf)[kNB], uint8_t* smem,
                                                 ChainSync* sy) {
+    lds_wait_ge(&sy->io_mark, (uint32_t)(2 * s));  // the stage's input rows have landed
     const ChainStage st = c_desc(p, s);
     const int wave = c_wave(), b = blockIdx.x;
     const int astride = p.kp_max + 16;
     const int E = c_row_items(st, c_items(st, b)) * st.steps;
     int* accg = reinterpret_cast<int*>(smem + p.off_acc);
     int* accu = accg + p.ipw_max * 16 * MR;
-    lds_wait_ge(&sy->rows_ready, (uint32_t)(s + 1));
-    // the host keeps every stage within one load of the compute waves (E <= kCW * kCMaxE)
     const int f0 = E * wave / kCW, f1 = E * (wave + 1) / kCW;
-    c_compute<MR>(buf, st, b, f0, f1 - f0, smem, astride, p.M, accg, accu);
+    for (int r0 = f0;;) {
+        const int cnt = min(f1 - r0, kCMaxE);
+        c_load<0, kCMaxE>(buf, st, b, r0, cnt);
+        if (r0 == f0) lds_wait_ge(&sy->rows_ready, (uint32_t)(s + 1));
+        c_compute<MR>(buf, st, b, r0, cnt, smem, astride, p.M, accg, accu);
+        r0 += cnt;
+        if (r0 >= f1) break;
+    }
     wait_lds();  // the sums are in LDS before this wave counts itself done
     if ((threadIdx.x & 63) == 0) atomicAdd(&sy->done, 1u);
-    if (s + 1 < p.n_stages) {
-        // The next stage's weight loads wait until its input rows are in LDS.  Loads in
-        // flight during the exchange sit ahead of the exchange's own loads and stores in
-        // this CU's memory pipeline: issued right after the products, or half of them
-        // then, the 36-layer stack ran 1.2x / 1.13x slower than issued here.
-        lds_wait_ge(&sy->io_mark, (uint32_t)(2 * s + 2));
-        c_load_stage<0, kCMaxE>(p, s + 1, buf);
-    }
 }
 
 template <int MR>
@@ -600,7 +593,6 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainParams p) {
     __syncthreads();  // the only workgroup barrier
     if (tid < 64 * kCW) {
         v4i buf[kNB];
-        c_load_stage<0, kCMaxE>(p, 0, buf);
         for (int s = 0; s < p.n_stages; ++s) {
             c_stage_compute<MR>(p, s, buf, smem, &sy);
         }

@@ -67,7 +67,5 @@ struct ChainParams {
 size_t chain_lds_layout(int max_rows, int kp_max, int k_max, int kg_max, int ipw_max, ChainParams* p);
 hipError_t launch_chain(const ChainParams& p, int grid, size_t lds, hipStream_t stream);
 int chain_resident_per_cu(int max_rows, size_t lds);  // workgroups of the chain kernel per CU
-// Largest weight steps one workgroup round takes for a stage of this kind.
-int chain_round_capacity();
 
 }  // namespace qlin

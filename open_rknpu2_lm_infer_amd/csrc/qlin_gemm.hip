@@ -14,8 +14,9 @@
 // one instruction fills 1 KiB of LDS in lane order, and which global 16-byte chunk a
 // lane fetches sets the XOR swizzle that keeps fragment reads free of bank conflicts.
 // gfx950 LDS has 64 banks of 4 bytes and a ds_read_b128 takes four cycles of 16 lanes;
-// which lanes share a cycle was probed pattern by pattern (probes/hw_probes.hip, lds,
-// under SQ_LDS_BANK_CONFLICT).  The swizzles used here read with zero conflicts there:
+// which lanes share a cycle was measured one access pattern at a time with calibration
+// kernels under SQ_LDS_BANK_CONFLICT.  The swizzles used here read with zero conflicts there
+// (and the counter reads 0 for this kernel):
 // 128-byte rows (A, W8) XOR the chunk with bit 1 of the row into chunk bit 0 and bit 2
 // into chunk bit 2; 64-byte rows (W4) XOR it with (row >> 1) & 3.
 // A row beyond M or N lies past its buffer descriptor's size and arrives as zero.

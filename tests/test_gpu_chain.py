@@ -217,8 +217,9 @@ def test_chain_nonfinite_status():
 def test_chain_wait_give_up_and_recover(ws):
     """A stage wait that gives up (forced from the host with a wait limit of zero polls:
     every kernel still exits normally) is reported as QLIN_ERR_DEVICE by qlin_chain_status,
-    which also restarts the stage counters; the same chain then runs correctly again with
-    the default limit (src/model/dense.rs:398-540 stages, two layers)."""
+    which reads and clears the error word.  A run that gave up leaves no state behind: the
+    next launch's epoch makes every completion flag fresh, so the same chain then runs
+    correctly again with the default limit (src/model/dense.rs:398-540 stages, two layers)."""
     gam = [synth.gamma(synth.HIDDEN, seed=940 + i).to(DEV) for i in range(4)]
     s0, h0 = qwen_layer_stages(0, gam[:2])
     s1, h1 = qwen_layer_stages(1, gam[2:])
@@ -289,4 +290,27 @@ def test_chain_swiglu_any_even_width(oracle, ws):
     for s, (st, host) in enumerate(zip(stages, (wa, wb, wc))):
         expect = oracle_linear(oracle, ins[s].cpu(), host[1], host[2], bool(st["flags"] & ql.QLIN_SWIGLU))
         check_outputs(oracle, outs[s], expect, bool(st["flags"] & ql.QLIN_SWIGLU), torch.float16)
+    chain.close()
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_chain_w8_gate_up_in_rounds(oracle, ws, rows):
+    """All-W8 Qwen3-4B MLP: RMSNorm -> gate_up (W8, K=2560, N=19456, SiLU-gate) -> down (W8).
+    The gate_up share of a CU is 120 weight steps, more than the 80 the compute waves hold
+    in registers, so the stage streams in two rounds; every stage equals the single-linear
+    launch bit for bit, and the gate_up stage the oracle (src/npu.rs:1052-1062 W8 path)."""
+    (_, Kg, Ng), (_, Kd, Nd) = synth.LAYER[2], synth.LAYER[3]
+    wg = linear(8, Kg, Ng, synth.linear_seed(0, 2, workload=8), stack=True)
+    wd = linear(8, Kd, Nd, synth.linear_seed(0, 3, workload=8), stack=True)
+    gam = synth.gamma(synth.HIDDEN, seed=990).to(DEV)
+    stages = [dict(weights=wg[0], flags=ql.QLIN_SWIGLU, gamma=gam, eps=1e-6, input=-1, offset=0),
+              dict(weights=wd[0], flags=0, input=0, offset=0)]
+    chain = ql.Chain(stages, max_rows=rows)
+    x = synth.activations(rows, synth.HIDDEN, seed=991 + rows, device=DEV)
+    y = chain.run(x)
+    torch.cuda.synchronize()
+    assert chain.status() == 0
+    ins, outs = check_against_single(ws, chain, stages, x, y, rows)
+    expect = oracle_linear(oracle, ins[0].cpu(), wg[1], wg[2], True, gamma=gam.cpu().numpy())
+    check_outputs(oracle, outs[0], expect, True, torch.float16)
     chain.close()

@@ -31,12 +31,10 @@ def cfg_ws(cfg, rows, K, N, splits=None):
         os.environ.pop("QLIN_GEMM_SPLITS", None)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
-@pytest.mark.parametrize("bits", [4, 8])
+# every (configuration, bits) pair the kernel has: configuration 3 exists for W4 only
+@pytest.mark.parametrize("cfg,bits", [(c, b) for b in (4, 8) for c in ((0, 1, 2, 3) if b == 4 else (0, 1, 2))])
 @pytest.mark.parametrize("K,N,M,splits", [(2560, 1024, 300, None), (4096, 640, 17, 3), (1024, 2000, 513, 2)])
 def test_gemm32_configs_match_oracle(oracle, cfg, bits, K, N, M, splits):
-    if cfg == 3 and bits == 8:
-        pytest.skip("configuration 3 is W4 only")
     codes = synth.codes(N, K, bits, 600 + cfg + K % 7 + bits).numpy()
     sc = synth.scales(N, bits, 601 + bits).numpy()
     w = make_weights(bits, codes, sc)

@@ -129,6 +129,35 @@ def test_rmsnorm_quantize_many_rows(oracle, dtype, order, M, K):
     assert not qh[:, K:].any()  # the zero tail up to ldq
 
 
+# every register-resident instance of the one-wave-per-row RMSNorm kernel: chunks of 16
+# bytes per lane NC = 2, 4, 5, 8 for fp16 (chain-major sum when K % 512 == 0 in the chain
+# order, row-major otherwise) and f32 rows
+@pytest.mark.parametrize("order", ["neon16", "seq"])
+@pytest.mark.parametrize("dtype,K", [
+    (torch.float16, 1024),  # NC 2, chain-major
+    (torch.float16, 1536),  # NC 3 -> 4, chain-major
+    (torch.float16, 2000),  # NC 4, row-major (K % 512 != 0)
+    (torch.float16, 4096),  # NC 8, chain-major
+    (torch.float32, 1024),  # NC 4
+    (torch.float32, 1280),  # NC 5
+    (torch.float32, 2048),  # NC 8
+])
+def test_rmsnorm_quantize_many_rows_register_paths(oracle, order, dtype, K):
+    M = 1024
+    x = synth.activations(M, K, seed=K + 3, device="cpu", dist="student_t3").to(dtype)
+    gam = synth.gamma(K, seed=K + 1, device="cpu")
+    flags = ql.QLIN_NORM_SEQUENTIAL if order == "seq" else 0
+    ldq = roundup(K, 256)
+    q, s = ql.quantize(x.to(DEV), ldq=ldq, gamma=gam.to(DEV), eps=1e-6, flags=flags)
+    torch.cuda.synchronize()
+    y = oracle.rmsnorm(x.float().numpy(), gam.numpy(), 1e-6, order)
+    qo, so, _ = oracle.quantize(y)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    qh = q.cpu().numpy()
+    assert np.array_equal(qh[:, :K], qo)
+    assert not qh[:, K:].any()
+
+
 @pytest.mark.parametrize("dtype,K", [(torch.float16, 2560), (torch.float16, 104), (torch.float32, 2560)])
 def test_rmsnorm_quantize_many_rows_nonfinite(oracle, dtype, K):
     """Rows holding NaN, Inf or -Inf among 1030 RMSNorm rows (fp16 K = 2560: the chain-major

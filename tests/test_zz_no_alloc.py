@@ -59,6 +59,49 @@ def test_noalloc_matches_workspace_entry(bits, K, N, swiglu, norm, rows):
     w.close()
 
 
+@pytest.mark.parametrize("bits,K,N,swiglu,norm,M", [
+    (4, 2560, 19456, True, True, 1),     # fused decode GEMV with RMSNorm and SiLU-gate
+    (8, 9728, 2560, False, False, 512),  # prefill GEMM with split-K (counters reused per replay)
+])
+def test_noalloc_under_graph_capture(bits, K, N, swiglu, norm, M):
+    """qlin_run_noalloc captured in a HIP graph (the callers it is for), replayed with a
+    new input each time and eager workspace runs between the replays: every replay equals
+    qlin_run bit for bit."""
+    w = weights(bits, K, N, 820 + bits)
+    ws = ql.Workspace(M, K, N)
+    gamma = synth.gamma(K, seed=821, device=DEV) if norm else None
+    flags = ql.QLIN_SWIGLU if swiglu else 0
+    ncols = N // 2 if swiglu else N
+    A = synth.activations(M, K, seed=822, device=DEV)
+    out = torch.empty((M, ncols), dtype=torch.float16, device=DEV)
+    lib = _lib.load()
+
+    def call():
+        return lib.qlin_run_noalloc(w.handle, M, ql._ptr(A), ql.QLIN_F16, A.stride(0),
+                                    ql._ptr(gamma) if gamma is not None else None, 1e-6, ql._ptr(out), ql.QLIN_F16,
+                                    out.stride(0), flags, None, ql._stream())
+
+    assert call() == 0  # eager first: code objects load outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = call()
+    assert rc == 0
+    for rep in range(4):
+        print(f"[noalloc graph] bits={bits} K={K} N={N} M={M} replay {rep}", flush=True)
+        A.copy_(synth.activations(M, K, seed=823 + rep, device=DEV))
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = ql.run(ws, w, A, flags=flags, gamma=gamma, eps=1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (rep, (got != ref).sum().item())
+    del g
+    ws.close()
+    w.close()
+
+
 def test_noalloc_error_word_and_limits():
     w = weights(4, 2560, 1024, 810)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
