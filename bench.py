@@ -402,6 +402,7 @@ def main():
     # ---------------------------------------------------------------- per-kernel (graph, events)
     # each projection rotates >= 512 MB of copies (layer copies plus extra ones)
     per_kernel = {}
+    pools = []
     for p, (name, K, N) in enumerate(synth.LAYER):
         b = N * K // 2 + N * 4
         n_copies = max(L, -(-ROTATE_BYTES // b))
@@ -418,9 +419,44 @@ def main():
                             "copies_rotated": len(pool), "rotated_bytes": b * len(pool)}
         log(f"  gemv {name}: {us:.2f} us/launch, {per_kernel[name]['gbs']} GB/s ({len(pool)} copies)")
         del g
+        pools.append(pool)
+    dom = per_kernel["gate_up"]
+
+    # ---------------------------------------------------------------- decode at M = 2, 4, 8 rows
+    # (the speculative-verify batch of 1 + up to 7 draft tokens, src/model/speculation.rs:36,51):
+    # the same layer step and per-projection rotation as M = 1
+    decode_rows = {}
+    for M in (2, 4, 8):
+        acts_m = [synth.activations(M, K, seed=synth.linear_seed(0, p) + 10 + M, device=dev)
+                  for p, (_, K, _) in enumerate(synth.LAYER)]
+        outs_m = [torch.empty((M, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+                  for name, K, N in synth.LAYER]
+        line = {}
+        for p, (name, K, N) in enumerate(synth.LAYER):
+            pool = pools[p]
+            g = capture(lambda i, p=p, pool=pool: ql.run(ws, pool[i % len(pool)], acts_m[p], out=outs_m[p],
+                                                         flags=flags[p]), len(pool))
+            r = max(2, args.kernel_reps)
+            us = time_graph(g, r) * 1e6 / (r * len(pool))
+            del g
+            line[name] = {"us": round(us, 3), "gbs": round(per_kernel[name]["bytes"] / (us * 1e-6) / 1e9, 1)}
+
+        def step_m(i, acts_m=acts_m, outs_m=outs_m):
+            for p in range(4):
+                ql.run(ws, layers[i % L][p], acts_m[p], out=outs_m[p], flags=flags[p])
+
+        g = capture(step_m, L)
+        r = max(2, args.kernel_reps)
+        us_l = time_graph(g, r) * 1e6 / (r * L)
+        del g
+        decode_rows[f"m{M}"] = {"layer_us": round(us_l, 2), "layer_gbs": round(bytes_layer / (us_l * 1e-6) / 1e9, 1),
+                                "frac_of_hbm": round(bytes_layer / (us_l * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "per_proj": line, "rounding": "half_away"}
+        log(f"  decode layer M={M}: {us_l:.2f} us/step ({decode_rows[f'm{M}']['layer_gbs']} GB/s); " +
+            ", ".join(f"{n} {v['us']:.2f}" for n, v in line.items()))
+    for pool in pools:
         for w in pool[L:]:
             w.close()
-    dom = per_kernel["gate_up"]
 
     # ---------------------------------------------------------------- W8 GEMV, M=1, K=N=2560
     K1 = N1 = 2560
@@ -433,12 +469,13 @@ def main():
         del packed, codes, sc
     x1 = synth.activations(1, K1, seed=synth.linear_seed(0, 0, workload=1) + 1, device=dev)
     y1 = torch.empty((1, N1), dtype=torch.float16, device=dev)
-    g = capture(lambda i: ql.run(ws, w8[i % n1], x1, out=y1), n1)
+    g = capture(lambda i: ql.run(ws, w8[i % n1], x1, out=y1, flags=ql.QLIN_ROUND_HALF_EVEN), n1)
     r = max(2, args.kernel_reps)
     us = time_graph(g, r) * 1e6 / (r * n1)
     w8_line = {"workload": "W8A8 GEMV M=1 K=N=2560, int8 codes U[-127,127], scales U(0.002,0.02)",
                "us": round(us, 3), "bytes": b1, "gbs": round(b1 / (us * 1e-6) / 1e9, 1),
-               "frac_of_hbm": round(b1 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies_rotated": n1}
+               "frac_of_hbm": round(b1 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies_rotated": n1,
+               "rounding": "half_to_even"}
     log(f"  W8 GEMV 2560x2560 M=1: {us:.2f} us/launch, {w8_line['gbs']} GB/s ({n1} copies)")
     del g
     for w in w8:
@@ -459,7 +496,7 @@ def main():
         tot_ops += ops
         tot_us += us
         tot_gemm_us += us_g
-        prefill[name] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+        prefill[name] = {"rounding": "half_away", "us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
                          "gemm_us": round(us_g, 2), "gemm_tops": round(ops / (us_g * 1e-6) / 1e12, 1)}
         log(f"  prefill M=512 {name}: {us:.1f} us, {prefill[name]['tops']} TOPS (quant + GEMM); "
             f"GEMM alone {us_g:.1f} us, {prefill[name]['gemm_tops']} TOPS")
@@ -474,6 +511,30 @@ def main():
         "frac": round(prefill[dom_p]["gemm_tops"] / INT8_PEAK_TOPS, 4), "ops_per_launch": dom_ops,
         "us_per_launch": prefill[dom_p]["gemm_us"],
     }
+
+    # ---------------------------------------------------------------- M=128 (the reference's ubatch)
+    # The only path figures the reference publishes are RK3588 times at M=128 (quantize, NPU
+    # GEMM, reduce and dequant per call); they sit beside these as context, not as a target.
+    ref_m128_ms = {"gate_up": 6.731, "o": 1.561, "down": 3.132}
+    M128 = 128
+    acts128 = [synth.activations(M128, K, seed=synth.linear_seed(0, p) + 3, device=dev)
+               for p, (_, K, _) in enumerate(synth.LAYER)]
+    outs128 = [torch.empty((M128, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
+               for name, K, N in synth.LAYER]
+    m128 = {"rounding": "half_away", "context_ref_rk3588_ms": {
+        "gate_up": "6.731 (W4A8 + fused SwiGLU, llm_generated_docs/QWEN3_W4A8_N_PIPELINE_20261020.md:10)",
+        "o": "1.561 (llm_generated_docs/QWEN3_W4A8_UTILIZATION_20261020.md:26)",
+        "down": "3.132 (llm_generated_docs/QWEN3_W4A8_UTILIZATION_20261020.md:27)"}}
+    for p, (name, K, N) in enumerate(synth.LAYER):
+        g = capture(lambda i, p=p: ql.run(ws, layers[i % L][p], acts128[p], out=outs128[p], flags=flags[p]), L)
+        r = max(1, args.prefill_reps)
+        us = time_graph(g, r) * 1e6 / (r * L)
+        del g
+        ops = 2.0 * M128 * N * K
+        m128[name] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+        if name in ref_m128_ms:
+            m128[name]["ref_over_this"] = round(ref_m128_ms[name] * 1e3 / us, 1)
+        log(f"  M=128 {name}: {us:.1f} us, {m128[name]['tops']} TOPS (quant + GEMM)")
 
     # ---------------------------------------------------------------- W8 lm_head at M=1
     # 151,936 x 2560 int8 (389 MB, larger than the Infinity Cache): one GEMV launch.
@@ -490,7 +551,7 @@ def main():
         r = max(1, args.head_reps)
         us = time_graph(g, r) * 1e6 / (r * 4)
         hb = Nh * Kh + Nh * 4
-        head = {"us": round(us, 2), "bytes": hb, "gbs": round(hb / (us * 1e-6) / 1e9, 1),
+        head = {"rounding": "half_away", "us": round(us, 2), "bytes": hb, "gbs": round(hb / (us * 1e-6) / 1e9, 1),
                 "frac_of_hbm": round(hb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"  lm_head W8 151936x2560 M=1: {us:.1f} us, {head['gbs']} GB/s")
         del g
@@ -564,6 +625,7 @@ def main():
             same = bool(torch.equal(yc, h_last)) and bool(torch.isfinite(h_last.float()).all())
             chain.close()
             stack[f"m{M}"] = {
+                "rounding": "half_away",
                 "launches_us": round(us_l, 1), "launches_gbs": round(stack_bytes / (us_l * 1e-6) / 1e9, 1),
                 "chain_us": round(us_c, 1), "chain_gbs": round(stack_bytes / (us_c * 1e-6) / 1e9, 1),
                 "chain_equals_launches": same and ok,
@@ -600,7 +662,7 @@ def main():
             log(f"  prefill M=4096 {name}: {us:.1f} us, {per[name]['tops']} TOPS"
                 f"{' (RMSNorm + quant + GEMM)' if gam_l[p] is not None else ' (quant + GEMM)'}")
             del g
-        long_prefill = {"tops": round(tot_ops / (tot_us * 1e-6) / 1e12, 1),
+        long_prefill = {"rounding": "half_away", "tops": round(tot_ops / (tot_us * 1e-6) / 1e12, 1),
                         "frac_of_int8_peak": round(tot_ops / (tot_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
                         "us_per_layer": round(tot_us, 1), "per_proj": per}
         ws_l.close()
@@ -622,7 +684,7 @@ def main():
             if el >= args.cpu_seconds:
                 break
         cpu_gbs = bytes_layer * n_layers / el / 1e9
-        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port", "rounding": "half_away",
                "nproc": nproc, "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
                "sample": f"{n_layers} passes of the same M=1 W4 layer (4 linears, fp16 in/out) in "
                          f"{el:.1f} s with the C oracle (OpenMP on all {nproc} host cores available to the "
@@ -643,6 +705,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
+        "rounding": "half_away (activation quantization rounds half away from zero, src/npu.rs:1109; "
+                    "w8_gemv_2560 runs BASELINE config 1's half-to-even)",
         "data": "synthetic (seeded: W4 codes U[-8,7], scales U(0.01,0.1), fp16 N(0,1) activations with 1% x20 outlier channels)",
         "config": {
             "workload": "W4A8 decode GEMV over one Qwen3-4B layer (qkv 2560x6144, o 4096x2560, "
@@ -668,6 +732,8 @@ def main():
         "prefill_m512": {"tops": round(prefill_tops, 1), "frac_of_int8_peak": round(prefill_tops / INT8_PEAK_TOPS, 4),
                          "gemm_only_tops": round(prefill_gemm_tops, 1),
                          "per_proj": prefill},
+        "prefill_m128": m128,
+        "decode_rows": decode_rows,
         "lm_head_w8_m1": head,
         "decode_stack_mixed": stack,
         "prefill_m4096_rmsnorm": long_prefill,

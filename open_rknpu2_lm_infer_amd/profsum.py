@@ -86,7 +86,8 @@ def main(argv=None):
     ap.add_argument("--copy-match", default="copyBuffer")
     ap.add_argument("--copy-bytes", type=float)
     ap.add_argument("--md", action="store_true", help="stats as a markdown table with each kernel's share")
-    ap.add_argument("--chunk", type=int, default=0, help="pmc: split each kernel and grid into runs of N dispatches")
+    ap.add_argument("--chunk", type=int, default=0,
+                    help="pmc / traffic: split each kernel and grid into runs of N dispatches (traffic: one line each)")
     a = ap.parse_args(argv)
     if a.what == "stats" and a.md:
         rows = kernel_stats(a.db, a.match)
@@ -108,16 +109,26 @@ def main(argv=None):
             for c, v in sorted(d.items()):
                 print(f"    {c:32s} {v:16.2f}")
     else:
-        f_k = _one(a.fetch, "FETCH_SIZE", a.match)
-        w_k = _one(a.write, "WRITE_SIZE", a.match)
         f_c = _one(a.copy_fetch, "FETCH_SIZE", a.copy_match)
         w_c = _one(a.copy_write, "WRITE_SIZE", a.copy_match)
         kib = a.copy_bytes / 1024.0
         f_scale, w_scale = kib / f_c, kib / w_c
-        fetch_b = f_k * f_scale * 1024.0
-        write_b = w_k * w_scale * 1024.0
         print(f"copy of {a.copy_bytes:.0f} B: FETCH_SIZE {f_c:.1f} KiB (scale {f_scale:.4f}), "
               f"WRITE_SIZE {w_c:.1f} KiB (scale {w_scale:.4f})")
+        if a.chunk:
+            # every matched kernel and grid, split into runs of --chunk dispatches
+            fm, wm = pmc_means(a.fetch, a.match, a.chunk), pmc_means(a.write, a.match, a.chunk)
+            for name in fm:
+                if "FETCH_SIZE" not in fm[name] or "WRITE_SIZE" not in wm.get(name, {}):
+                    continue
+                fb = fm[name]["FETCH_SIZE"] * f_scale * 1024.0
+                wb = wm[name]["WRITE_SIZE"] * w_scale * 1024.0
+                print(f"{name[:110]}: fetch {fb:.0f} B, write {wb:.0f} B, traffic {fb + wb:.0f} B")
+            return 0
+        f_k = _one(a.fetch, "FETCH_SIZE", a.match)
+        w_k = _one(a.write, "WRITE_SIZE", a.match)
+        fetch_b = f_k * f_scale * 1024.0
+        write_b = w_k * w_scale * 1024.0
         print(f"kernel /{a.match}/: FETCH_SIZE {f_k:.1f} KiB -> {fetch_b:.0f} B, WRITE_SIZE {w_k:.1f} KiB -> {write_b:.0f} B")
         print(f"traffic_bytes_per_launch: {fetch_b + write_b:.0f}")
     return 0

@@ -51,7 +51,7 @@ def run_both(ws, w, A, **kw):
 # item counts: 300 and 1000 plain (2 and 4 per workgroup on 256 CUs), 700 SwiGLU (3 each)
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("N,swiglu", [(16 * 300, False), (16 * 1000, False), (2 * 16 * 700, True)])
-@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_items_match_oracle_and_single_item(oracle, ws, bits, N, swiglu, M):
     K = 1024 if bits == 8 else 2560
     codes = synth.codes(N, K, bits, 300 + bits).numpy()
@@ -180,3 +180,4 @@ def test_fused_rows_fewer_waves(oracle, bits, K, M):
         check_outputs(oracle, out, expect, False, torch.float16)
     w.close()
     ws.close()
+
