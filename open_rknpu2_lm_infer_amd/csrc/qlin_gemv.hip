@@ -40,13 +40,17 @@ constexpr int kFusedMaxRows = 4;
 
 // Register budget per wave count (1024-thread workgroups get 128 VGPRs per lane):
 // wave steps in flight per register buffer, and 8-element activation groups held
-// per thread by the fused prologue.
+// per thread by the fused prologue.  With RMSNorm each slot also holds its 8 gamma
+// values: 2 slots at 16 waves and 4 below (the f32 rows of the RMSNorm fit 64 KiB of LDS,
+// K <= 16384, i.e. at most 4 groups per thread at 512 threads), which keeps those
+// kernels from spilling.
 template <int WAVES, bool FUSED>
 struct GemvCfg {
     static constexpr int BATCH = FUSED ? (WAVES >= 8 ? 2 : 4) : (WAVES >= 16 ? 1 : 2);
-    static constexpr int XREGS = WAVES >= 16 ? 2 : 8;
+    static constexpr int XREGS = WAVES >= 16 ? 4 : 8;
+    static constexpr int XREGS_NORM = WAVES >= 16 ? 2 : 4;
 };
-constexpr int fused_regs(int waves) { return waves >= 16 ? 2 : 8; }
+constexpr int fused_regs(int waves, bool norm) { return waves >= 16 ? (norm ? 2 : 4) : (norm ? 4 : 8); }
 // Several rows with RMSNorm hold gamma per register slot as well: fewer slots keep the
 // prologue within the register file.
 constexpr int kNormRowsRegs = 4;
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = NORM && MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM) : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -612,7 +616,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = NORM && MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM) : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -952,7 +956,7 @@ int gemv_pick_waves(int groups, int steps) {
 bool gemv_can_fuse(int M, int K, int waves, bool norm) {
     const int nt = 64 * waves;
     const int gpt = (K / 8 + nt - 1) / nt;
-    if (K % 8 || M > kFusedMaxRows || M * gpt > fused_regs(waves)) return false;
+    if (K % 8 || M > kFusedMaxRows || M * gpt > fused_regs(waves, norm)) return false;
     if (norm && (size_t)M * K * 4 > 64 * 1024) return false;  // f32 rows of the RMSNorm in LDS
     // (1024-thread workgroups would spill the per-slot gamma registers)
     if (norm && M > 1 && (waves > 8 || M * gpt > kNormRowsRegs)) return false;
