@@ -309,8 +309,8 @@ typedef struct qlin_chain_stage {
 /* Checks the stages (K of each stage = the columns it reads; K % 8 == 0) and
  * allocates the intermediate fp16 buffers for max_rows <= 4 rows.  The weights must
  * outlive the chain.  A CU holds up to 80 steps of 128 weight bytes of a stage in
- * registers at once; a larger share (a W8 SiLU-gate stage K=2560, N=19456 takes 120 on
- * 256 CUs) streams in several rounds within the stage. */
+ * registers at once (64 for 2..4 rows); a larger share (a W8 SiLU-gate stage K=2560,
+ * N=19456 takes 120 on 256 CUs) streams in several rounds within the stage. */
 int qlin_chain_create(const qlin_chain_stage* stages, int32_t n_stages, int32_t max_rows,
                       qlin_chain** out);
 void qlin_chain_free(qlin_chain* chain);

@@ -12,14 +12,14 @@
 // workgroup (e.g. 10 of N = 2560 on 256 CUs).  An item is one 16-row MFMA tile over
 // the whole K; rows past the item's width re-read its last row and are not stored.
 //
-// Waves.  Four compute waves (one per SIMD) and four helper waves.  The compute waves
-// hold their workgroup's share of a stage's weights in registers (up to 40 x 16 bytes
-// per lane) and issue no other global memory access, so the only thing they ever wait
-// for is their own weight loads.  The helper waves do everything else: the first one
-// (the I/O wave) polls the previous stage's completion flags, copies the stage input
-// rows and the RMSNorm weights into LDS with direct global -> LDS copies and reads the
-// per-channel scales and residual rows; all four compute the RMSNorm, per-token scale
-// and quantized rows into LDS; after the products the I/O wave runs the epilogue and
+// Waves.  Four compute waves (one per SIMD) and four helper waves, eight for 2..4 rows
+// (ChainShape).  The compute waves hold their workgroup's share of a stage's weights in
+// registers (up to 40 x 16 bytes per lane, 32 for 2..4 rows) and issue no other global
+// memory access, so the only thing they ever wait for is their own weight loads.  The
+// helper waves do everything else: the first one (the I/O wave) polls the previous
+// stage's completion flags, copies the stage input rows and the RMSNorm weights into
+// LDS with direct global -> LDS copies and reads the per-channel scales and residual
+// rows; all helpers compute the RMSNorm, per-token scale and quantized rows into LDS; after the products the I/O wave runs the epilogue and
 // stores this workgroup's outputs.  The two groups never share a barrier: the compute
 // waves wait for LDS words (input rows landed, quantized rows ready) and count
 // themselves done in another; the helpers synchronize among themselves with an LDS
@@ -50,18 +50,11 @@
 namespace qlin {
 
 constexpr int kCW = kChainComputeWaves;
-constexpr int kHW = kChainHelperWaves;
-constexpr int kHT = 64 * kHW;  // helper threads
-constexpr int kCT = kChainThreadsPerBlock;
-constexpr int kNB = kChainBufRegs;
 constexpr int kSc1 = 16;  // cache policy: coherent at device scope
 constexpr int kRsrcFlags = 0x00020000;
 
 typedef unsigned int u32x4c __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* chain_lds_ptr;
-
-constexpr int kCMaxE = kNB / 2;  // weight steps a compute wave holds (two 16-byte loads each)
-
 
 // Wave index as a wave-uniform (scalar) value: offsets derived from it stay in SGPRs.
 __device__ __forceinline__ int c_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -106,8 +99,8 @@ __device__ __forceinline__ int c_row_items(const ChainStage& st, int n_it) {
 // 128-byte step of row r.  Every slot is loaded: slots past cnt read past the end of
 // the buffer resource, which returns zeros without a memory access, so buf is written
 // whole on one code path.
-template <int E0, int E1>
-__device__ __forceinline__ void c_load(v4i (&buf)[kNB], const ChainStage& st, int b, int f0, int cnt) {
+template <int E0, int E1, int NB>
+__device__ __forceinline__ void c_load(v4i (&buf)[NB], const ChainStage& st, int b, int f0, int cnt) {
     const int lane = threadIdx.x & 63;
     const bool sw = (st.flags & kFlagSwiglu) != 0;
     const __amdgpu_buffer_rsrc_t r = c_rsrc(st.W, (int64_t)st.Np * st.wrow);
@@ -149,8 +142,8 @@ __device__ __forceinline__ void c_flush(const ChainStage& st, int b, int ri, con
 // Matrix products of weight steps f0 .. f0 + cnt - 1 (already in buf) with the
 // quantized rows in LDS.  One code path for both widths (a uniform branch per step),
 // so the weight registers have a single consumer in the compute waves' loop.
-template <int MR>
-__device__ __forceinline__ void c_compute(const v4i (&buf)[kNB], const ChainStage& st, int b, int f0, int cnt,
+template <int MR, int NB>
+__device__ __forceinline__ void c_compute(const v4i (&buf)[NB], const ChainStage& st, int b, int f0, int cnt,
                                           const uint8_t* lds_q, int astride, int M, int* accg, int* accu) {
     const bool w4 = st.bits == 4;
     const int KS = w4 ? 256 : 128;
@@ -160,7 +153,7 @@ __device__ __forceinline__ void c_compute(const v4i (&buf)[kNB], const ChainStag
     v4i acc = {0, 0, 0, 0};
     bool pending = false;
 #pragma unroll
-    for (int e = 0; e < kCMaxE; ++e) {
+    for (int e = 0; e < NB / 2; ++e) {
         if (e < cnt) {
             const v4i w[2] = {buf[2 * e], buf[2 * e + 1]};
             v4i a[4];
@@ -192,7 +185,7 @@ __device__ __forceinline__ void c_compute(const v4i (&buf)[kNB], const ChainStag
 struct ChainSync {
     uint32_t rows_ready;  // stages whose quantized rows are in LDS
     uint32_t done;        // compute-wave completions, kCW per stage
-    uint32_t helpers;     // helper arrivals, kHW per helper barrier
+    uint32_t helpers;     // helper arrivals, one per helper wave per helper barrier
     uint32_t io_mark;     // 2s once stage s's input rows are in LDS (releases the compute
                           // waves' weight loads of stage s)
 };
@@ -209,12 +202,13 @@ __device__ __forceinline__ void lds_wait_ge(const uint32_t* w, uint32_t target) 
     while (lds_load(w) < target) __builtin_amdgcn_s_sleep(1);
 }
 
-// Barrier of the kHW helper waves; k counts this wave's helper barriers.
+// Barrier of the HW helper waves; k counts this wave's helper barriers.
+template <int HW>
 __device__ __forceinline__ void helper_sync(ChainSync* sy, uint32_t& k) {
     wait_lds();  // this wave's LDS writes are visible before it arrives
     ++k;
     if ((threadIdx.x & 63) == 0) atomicAdd(&sy->helpers, 1u);
-    lds_wait_ge(&sy->helpers, kHW * k);
+    lds_wait_ge(&sy->helpers, HW * k);
 }
 
 // Waits until every workgroup has finished its part of stage s (all flags == e).
@@ -382,11 +376,12 @@ __device__ __forceinline__ uint2 c_quant8(const float v[8], float im, bool fast,
 
 // Helper waves: RMSNorm scale, per-token scale and the quantized rows of the stage
 // input (raw fp16 rows in LDS at off_x) into lds_q.  Same arithmetic as the GEMV
-// prologue.  h = helper thread index (0 .. kHT - 1).
+// prologue.  h = helper thread index (0 .. 64 * helper waves - 1).
 template <int MR>
 __device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStage& st, uint8_t* smem, int astride,
                                            int h, ChainSync* sy, uint32_t& hk, float* s_inv, float* s_rows,
                                            float (*s_red)[4], int* s_bad) {
+    constexpr int HW = ChainShape<MR>::kHelperWaves, HT = 64 * HW;
     const int hw = h >> 6, lane = h & 63;
     const int M = p.M, K = st.K, ng = K >> 3;
     const int xs = p.xstride >> 1;  // elements per LDS row
@@ -405,7 +400,7 @@ __device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStag
                 sum = c_sumsq_neon16(xrow, K);  // src/model/cpu.rs:14-35
             if (lane == 0) s_inv[hw] = 1.0f / __builtin_sqrtf(sum / (float)K + st.eps);
         }
-        helper_sync(sy, hk);
+        helper_sync<HW>(sy, hk);
     }
     float nsc[MR];
 #pragma unroll
@@ -417,7 +412,7 @@ __device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStag
     for (int m = 0; m < MR; ++m) {
         mx[m] = 0.0f;
         if (m < M) {
-            for (int g = h; g < ng; g += kHT) {
+            for (int g = h; g < ng; g += HT) {
                 float v[8];
                 c_unpack8(*reinterpret_cast<const uint4*>(lx + m * xs + 8 * g), v);
 #pragma unroll
@@ -435,18 +430,18 @@ __device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStag
     }
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) s_bad[hw] = any_bad;
-    helper_sync(sy, hk);
+    helper_sync<HW>(sy, hk);
     // 3. per-token scales, computed by every helper thread from the wave maxima
     int b = 0;
 #pragma unroll
-    for (int w = 0; w < kHW; ++w) b |= s_bad[w];
+    for (int w = 0; w < HW; ++w) b |= s_bad[w];
     float inv[MR];
     bool finite = true;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         float am = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kHW; ++w) am = fmaxf(am, s_red[w][m]);
+        for (int w = 0; w < HW; ++w) am = fmaxf(am, s_red[w][m]);
         const float sc = qscale_from_absmax(am);  // src/npu.rs:1101-1106
         finite &= __builtin_isfinite(sc);
         inv[m] = 1.0f / sc;
@@ -460,18 +455,18 @@ __device__ __forceinline__ void c_prologue(const ChainParams& p, const ChainStag
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         if (m < M) {
-            for (int g = h; g < ng; g += kHT) {
+            for (int g = h; g < ng; g += HT) {
                 float v[8];
                 c_unpack8(*reinterpret_cast<const uint4*>(lx + m * xs + 8 * g), v);
                 if (norm) c_norm8(v, lg, g, nsc[m]);
                 *reinterpret_cast<uint2*>(lds_q + m * astride + 8 * g) = c_quant8(v, inv[m], fast, rne);
             }
             // zeros in [K, Kp): a previous stage may have left a longer row here
-            for (int k = K + h * 8; k < st.Kp; k += kHT * 8)
+            for (int k = K + h * 8; k < st.Kp; k += HT * 8)
                 *reinterpret_cast<uint2*>(lds_q + m * astride + k) = make_uint2(0, 0);
         }
     }
-    helper_sync(sy, hk);
+    helper_sync<HW>(sy, hk);
 }
 
 // I/O wave, after the products: dequant / SiLU-gate / residual epilogue of this
@@ -531,7 +526,7 @@ __device__ __forceinline__ void c_stage_helpers(const ChainParams& p, int s, uin
     const bool io = h < 64;
     const int n_it = c_items(st, b);
     if (io) c_io_input<SW, MR>(p, st, s, b, n_it, e, smem, sy);
-    helper_sync(sy, hk);
+    helper_sync<ChainShape<MR>::kHelperWaves>(sy, hk);
     c_prologue<MR>(p, st, smem, p.kp_max + 16, h, sy, hk, s_inv, s_rows, s_red, s_bad);
     if (io) {
         if (h == 0) __hip_atomic_store(&sy->rows_ready, (uint32_t)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -545,11 +540,11 @@ __device__ __forceinline__ void c_stage_helpers(const ChainParams& p, int s, uin
 // and stores in this CU's memory pipeline (issued right after the previous stage's
 // products, or half of them then, the 36-layer stack ran 1.2x / 1.13x slower).  A share
 // longer than the registers hold (e.g. a W8 SiLU-gate stage: K = 2560, N = 19456 is 120
-// steps per CU) runs in rounds of kCMaxE steps, each loaded once the previous round's
+// steps per CU) runs in rounds of NB / 2 steps, each loaded once the previous round's
 // products are done.  The loads have one site in the code, so the weight registers have
 // a single owner (a second site made the compiler spill them).
-template <int MR>
-__device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i (&buf)[kNB], uint8_t* smem,
+template <int MR, int NB>
+__device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i (&buf)[NB], uint8_t* smem,
                                                 ChainSync* sy) {
     lds_wait_ge(&sy->io_mark, (uint32_t)(2 * s));  // the stage's input rows have landed
     const ChainStage st = c_desc(p, s);
@@ -560,8 +555,8 @@ __device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i
     int* accu = accg + p.ipw_max * 16 * MR;
     const int f0 = E * wave / kCW, f1 = E * (wave + 1) / kCW;
     for (int r0 = f0;;) {
-        const int cnt = min(f1 - r0, kCMaxE);
-        c_load<0, kCMaxE>(buf, st, b, r0, cnt);
+        const int cnt = min(f1 - r0, NB / 2);
+        c_load<0, NB / 2>(buf, st, b, r0, cnt);
         if (r0 == f0) lds_wait_ge(&sy->rows_ready, (uint32_t)(s + 1));
         c_compute<MR>(buf, st, b, r0, cnt, smem, astride, p.M, accg, accu);
         r0 += cnt;
@@ -572,11 +567,12 @@ __device__ __forceinline__ void c_stage_compute(const ChainParams& p, int s, v4i
 }
 
 template <int MR>
-__global__ __launch_bounds__(kCT) void chain_kernel(ChainParams p) {
+__global__ __launch_bounds__(ChainShape<MR>::kThreads) void chain_kernel(ChainParams p) {
+    constexpr int kCT = ChainShape<MR>::kThreads, kNB = ChainShape<MR>::kBufRegs;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_inv[4], s_rows[4];
-    __shared__ float s_red[kHW][4];
-    __shared__ int s_bad[kHW];
+    __shared__ float s_red[ChainShape<MR>::kHelperWaves][4];
+    __shared__ int s_bad[ChainShape<MR>::kHelperWaves];
     __shared__ ChainSync sy;
     const int tid = threadIdx.x, b = blockIdx.x;
     const int astride = p.kp_max + 16;
@@ -594,7 +590,7 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainParams p) {
     if (tid < 64 * kCW) {
         v4i buf[kNB];
         for (int s = 0; s < p.n_stages; ++s) {
-            c_stage_compute<MR>(p, s, buf, smem, &sy);
+            c_stage_compute<MR, kNB>(p, s, buf, smem, &sy);
         }
     } else {
         // the helpers' instructions (the exchange between stages) issue ahead of the
@@ -647,7 +643,8 @@ int chain_resident_per_cu(int max_rows, size_t lds) {
     const void* f = max_rows <= 1 ? reinterpret_cast<const void*>(&chain_kernel<1>)
                                   : reinterpret_cast<const void*>(&chain_kernel<4>);
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kCT, lds) != hipSuccess) return 0;
+    const int threads = max_rows <= 1 ? ChainShape<1>::kThreads : ChainShape<4>::kThreads;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, lds) != hipSuccess) return 0;
     return n;
 }
 
@@ -656,12 +653,12 @@ hipError_t launch_chain(const ChainParams& p, int grid, size_t lds, hipStream_t 
         static const hipError_t a1 = hipFuncSetAttribute(reinterpret_cast<const void*>(&chain_kernel<1>),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds);
         if (a1 != hipSuccess) return a1;
-        chain_kernel<1><<<grid, kCT, lds, stream>>>(p);
+        chain_kernel<1><<<grid, ChainShape<1>::kThreads, lds, stream>>>(p);
     } else {
         static const hipError_t a4 = hipFuncSetAttribute(reinterpret_cast<const void*>(&chain_kernel<4>),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kChainMaxLds);
         if (a4 != hipSuccess) return a4;
-        chain_kernel<4><<<grid, kCT, lds, stream>>>(p);
+        chain_kernel<4><<<grid, ChainShape<4>::kThreads, lds, stream>>>(p);
     }
     return hipGetLastError();
 }

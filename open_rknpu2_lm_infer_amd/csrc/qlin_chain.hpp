@@ -8,11 +8,21 @@
 namespace qlin {
 
 constexpr int kChainComputeWaves = 4;  // waves that stream weights (one per SIMD)
-constexpr int kChainHelperWaves = 4;   // waves that exchange rows and quantize them
-constexpr int kChainThreadsPerBlock = 64 * (kChainComputeWaves + kChainHelperWaves);
 constexpr int kChainMaxLds = 159 * 1024;  // dynamic LDS cap: 160 KiB less the static words
-constexpr int kChainBufRegs = 40;         // 16-byte weight registers per compute lane
 constexpr int kChainFlagStride = 256;     // flag words per stage (>= grid, multiple of 256)
+
+// Wave shape of the chain kernel for MR rows (1 or 4).  The 4-row instance quantizes four
+// rows per stage, so it runs eight helper waves; three waves per SIMD then leave 168
+// VGPRs a lane, and its compute waves hold 32 weight registers instead of 40 (measured
+// on the 36-layer stack at 4 rows: 1746 us against 1866 us with four helpers; the 1-row
+// instance ran slower with eight, 1180 us against 1155 us).
+template <int MR>
+struct ChainShape {
+    static constexpr int kHelperWaves = MR > 1 ? 8 : 4;  // waves that exchange rows and quantize them
+    static constexpr int kBufRegs = MR > 1 ? 32 : 40;    // 16-byte weight registers per compute lane
+    static constexpr int kThreads = 64 * (kChainComputeWaves + kHelperWaves);
+    static constexpr int kMaxSteps = kBufRegs / 2;  // weight steps a compute wave holds per round
+};
 
 struct ChainStage {
     const uint8_t* W;       // packed weights [Np, wrow]
