@@ -266,9 +266,279 @@ struct XGroup<float> {
     }
 };
 
+// Register slot i of the fused prologue holds this thread's group j of row m, with
+// i = m * gpt + j (gpt groups per thread per row).  The (m, j) of every slot come from a
+// running count, wave-uniform values in scalar registers: i / gpt, with gpt known only
+// at run time, cost an integer division sequence per slot in every loop over the slots.
+template <int XR>
+struct GemvSlots {
+    int m[XR], j[XR];
+    __device__ __forceinline__ explicit GemvSlots(int gpt) {
+        int m0 = 0, j0 = 0;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            m[i] = m0;
+            j[i] = j0;
+            if (++j0 == gpt) {
+                j0 = 0;
+                ++m0;
+            }
+        }
+    }
+};
+
+// The value of v[m] for a wave-uniform row index m < MR.  A chain of selects from a
+// constant keeps the registers statically indexed (starting from v[0] the compiler
+// turned the chain into an indexed load and moved v to scratch memory).
+template <int MR>
+__device__ __forceinline__ float row_pick(const float (&v)[MR], int m) {
+    float r = 1.0f;
+#pragma unroll
+    for (int mm = 0; mm < MR; ++mm)
+        if (mm == m) r = v[mm];
+    return r;
+}
+
+// Activation groups of this thread into registers (and with RMSNorm the gamma values of
+// each held group).  Only owned groups are loaded.  These loads may sit in branches
+// because every weight load after them is unconditional: waits for them then count
+// exactly the weight loads issued later.
+template <int MR, int XR, int NT, bool NORM, typename T>
+__device__ __forceinline__ void gemv_load_rows(const GemvParams& p, XGroup<T> (&xr)[XR], float (&gr)[NORM ? XR : 1][8],
+                                               const GemvSlots<XR>& sl, int nreg, int ngroups) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+        if (i < nreg) {
+            const int g = tid + NT * sl.j[i];
+            if (g < ngroups) xr[i].load(reinterpret_cast<const T*>(p.A) + (int64_t)sl.m[i] * p.lda + 8 * g);
+        }
+    }
+    if constexpr (NORM) {
+        // rows share gamma: one copy per register slot keeps the indexing static
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int g = tid + NT * sl.j[i];
+            if (i < nreg && g < ngroups) {
+                const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
+                const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
+                gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
+                gr[i][4] = b.x; gr[i][5] = b.y; gr[i][6] = b.z; gr[i][7] = b.w;
+            }
+        }
+    }
+}
+
+// Per-token scales from the wave maxima s_red[m][w] and the wave flags s_bad[w]: lane
+// m * WAVES + w reads s_red[m][w], the WAVES lanes of a row take their max by DPP, and
+// every lane computes its row's scale and reciprocal, so one LDS read and one division
+// sequence serve all rows (read row by row, 4 rows of 16 maxima took 64 words and four
+// division pairs in every wave).  Wave 0 writes s_rows.  Returns whether any wave saw a
+// value that is not finite.  The whole wave must be active.
+template <int WAVES, int MR>
+__device__ __forceinline__ bool gemv_row_scales(const float (*s_red)[WAVES], const int* s_bad, int M, float (&inv)[MR],
+                                                float* s_rows) {
+    static_assert(MR * WAVES <= 64, "one lane per wave maximum");
+    const int lane = threadIdx.x & 63;
+    float am = lane < MR * WAVES ? (&s_red[0][0])[lane] : 0.0f;
+    const int bad = lane < WAVES ? s_bad[lane] : 0;
+    am = dpp_max_step<0xB1, 0xf>(am);  // quad_perm [1, 0, 3, 2]
+    am = dpp_max_step<0x4E, 0xf>(am);  // quad_perm [2, 3, 0, 1]: every lane of a quad holds its max
+    if constexpr (WAVES >= 8) am = dpp_max_step<0x141, 0xf>(am);   // row_half_mirror: 8-lane max
+    if constexpr (WAVES >= 16) am = dpp_max_step<0x140, 0xf>(am);  // row_mirror: 16-lane max
+    const float sc = qscale_from_absmax(am);  // src/npu.rs:1101-1106
+    const float iv = 1.0f / sc;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        inv[m] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, iv), m * WAVES));
+    const int row = lane / WAVES;
+    if (threadIdx.x < 64 && lane == row * WAVES && row < M && row < MR) s_rows[row] = sc;
+    return __ballot(bad) != 0;
+}
+
 // Quantized rows of the fused prologue into LDS for finite rows (quant_finite).
 template <int BITS, bool NORM, bool RNE, int MR, int XR, typename XG>
 __device__ __forceinline__ void gemv_quant_rows(const XG (&xr)[XR], const float (&gr)[NORM ? XR : 1][8],
+                                                const float (&nsc)[MR], const float (&inv)[MR], uint8_t* lds_a,
+                                                int astride, const GemvSlots<XR>& sl, int nreg, int ngroups, int tid,
+                                                int NT) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+        if (i < nreg) {
+            const int m = sl.m[i], g = tid + NT * sl.j[i];
+            if (g < ngroups) {
+                float v[8];
+                xr[i].get(v);
+                if constexpr (NORM) {
+                    const float ns = row_pick(nsc, m);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
+                }
+                const float im = row_pick(inv, m);
+                int q[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) q[e] = quant_finite<RNE>(v[e], im);  // src/npu.rs:1107-1110
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                    w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                }
+                *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
+            }
+        }
+    }
+}
+
+// The fused prologue: (RMSNorm scale,) per-token scale and quantized rows in LDS.  LDS
+// rows 0..M-1 hold the quantized activations; row M is all zeros and feeds the
+// matrix-core rows M..15.  The caller's barrier after it publishes the rows.
+template <int BITS, int MODE, bool NORM, int WAVES, int MR, int XR, typename T>
+__device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const XGroup<T> (&xr)[XR],
+                                                    const float (&gr)[NORM ? XR : 1][8], const GemvSlots<XR>& sl,
+                                                    int nreg, int ngroups, uint8_t* smem, int astride, float* s_inv,
+                                                    float (*s_red)[WAVES], int* s_bad, float* s_rows) {
+    constexpr int NT = 64 * WAVES;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t* lds_a = smem;
+    const bool rne = (p.flags & kFlagRne) != 0;
+    float nsc[MR];  // RMSNorm scale per row
+#pragma unroll
+    for (int m = 0; m < MR; ++m) nsc[m] = 1.0f;
+    if constexpr (NORM) {
+        // the reference summation order needs each whole row in one place: f32 rows
+        // [M][K] in LDS, one wave per row
+        float* lds_x = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int m = MR == 1 ? 0 : sl.m[i], g = tid + NT * sl.j[i];
+            if (i < nreg && g < ngroups) {
+                float v[8];
+                xr[i].get(v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) lds_x[m * p.K + 8 * g + e] = v[e];
+            }
+        }
+        lds_barrier();
+        if (wave < p.M) {
+            const float* xm = lds_x + wave * p.K;
+            const float sum = (p.flags & kFlagNormSeq) != 0 ? (lane == 0 ? lds_sumsq_seq(xm, p.K) : 0.0f)  // src/ops/norm.rs:38
+                                                            : lds_sumsq_neon16(xm, p.K);  // src/model/cpu.rs:14-35
+            if (lane == 0) s_inv[wave] = 1.0f / __builtin_sqrtf(sum / (float)p.K + p.eps);
+        }
+        lds_barrier();
+#pragma unroll
+        for (int m = 0; m < MR; ++m) nsc[m] = m < p.M ? s_inv[m] : 1.0f;
+        lds_barrier();  // lds_x is overwritten by the quantized rows below
+    }
+    const bool owner_wave = wave * 64 < ngroups;  // waves holding activation groups (uniform)
+    if (owner_wave) {
+        float mx[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+        int bad = 0;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            if (i < nreg) {
+                const int m = sl.m[i], g = tid + NT * sl.j[i];  // m is uniform
+                if (g < ngroups) {
+                    float lm;
+                    if constexpr (MODE == 1 && !NORM) {
+                        // fp16 rows: absmax and finiteness from the bit patterns
+                        const uint4 r = xr[i].raw;
+                        const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
+                        bad |= mb > 0x7bffu;
+                        lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                    } else {
+                        float v[8];
+                        xr[i].get(v);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
+                        if constexpr (NORM) {
+                            const float ns = row_pick(nsc, m);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
+                        }
+                        lm = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) lm = fmaxf(lm, fabsf(v[e]));
+                        bad |= !__builtin_isfinite(lm);  // the normalized values must stay finite too
+                    }
+#pragma unroll
+                    for (int mm = 0; mm < MR; ++mm)
+                        if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float w = m < p.M ? wave_max_nonneg(mx[m]) : 0.0f;
+            if (lane == 0) s_red[m][wave] = w;
+        }
+        const bool any_bad = __ballot(bad) != 0;
+        if (lane == 0) s_bad[wave] = any_bad;
+    } else if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) s_red[m][wave] = 0.0f;
+        s_bad[wave] = 0;
+    }
+    lds_barrier();
+    // Per-token scales, computed by the waves that hold activation groups (the others
+    // go straight to the barrier instead of spending the SIMDs on scales they do not
+    // use) from all WAVES wave maxima (zeros, the identity of a max of magnitudes, from
+    // the waves that own no group).
+    if (owner_wave) {
+        float inv[MR];
+        const bool bad_rows = gemv_row_scales<WAVES, MR>(s_red, s_bad, p.M, inv, s_rows);
+        if (tid == 0 && bad_rows && p.err && blockIdx.x == 0) atomicOr(p.err, 1u);
+        if (!bad_rows) {
+            // finite rows (the usual case): the short rounding sequence
+            if (rne)
+                gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, sl, nreg, ngroups, tid, NT);
+            else
+                gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, sl, nreg, ngroups, tid, NT);
+        } else {
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                if (i < nreg) {
+                    const int m = sl.m[i], g = tid + NT * sl.j[i];
+                    if (g < ngroups) {
+                        float v[8];
+                        xr[i].get(v);
+                        if constexpr (NORM) {
+                            const float ns = row_pick(nsc, m);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
+                        }
+                        const float im = row_pick(inv, m);
+                        int q[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) q[e] = quant_one(v[e], im, rne);  // src/npu.rs:1107-1110
+                        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            w0 |= (uint32_t)(q[e] & 0xff) << (8 * e);
+                            w1 |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+                        }
+                        *reinterpret_cast<uint2*>(lds_a + m * astride + 8 * g) = make_uint2(w0, w1);
+                    }
+                }
+            }
+        }
+    }
+    // zero the K..Kp tail of each row and the whole zero row M
+    for (int m = 0; m < p.M; ++m)
+        for (int k = p.K + tid * 8; k < p.Kp; k += NT * 8)
+            *reinterpret_cast<uint2*>(lds_a + m * astride + k) = make_uint2(0, 0);
+    for (int k = tid * 16; k < p.Kp; k += NT * 16)
+        *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
+}
+
+// Quantized rows into LDS for finite rows (quant_finite), for the one-row prologue the
+// kernels keep written out: slot i holds group i - (i / gpt) * gpt of row i / gpt.
+template <int BITS, bool NORM, bool RNE, int MR, int XR, typename XG>
+__device__ __forceinline__ void gemv_quant_rows_1(const XG (&xr)[XR], const float (&gr)[NORM ? XR : 1][8],
                                                 const float (&nsc)[MR], const float (&inv)[MR], uint8_t* lds_a, int astride, int nreg, int gpt,
                                                 int ngroups, int tid, int NT) {
 #pragma unroll
@@ -356,7 +626,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const int ngroups = p.K >> 3;
     const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    if constexpr (FUSED) {
+    const GemvSlots<FUSED ? XR : 1> sl(gpt);
+    if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
         // weight loads issued after them.
@@ -381,6 +652,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                 }
             }
         }
+    } else if constexpr (FUSED) {
+        gemv_load_rows<MR, XR, NT, NORM>(p, xr, gr, sl, nreg, ngroups);
     } else {
         if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
     }
@@ -405,10 +678,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
     // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
     // LDS rows 0..M-1 hold the quantized activations; row M is all zeros and feeds
-    // the matrix-core rows M..15.
+    // the matrix-core rows M..15.  One row keeps its prologue written out here: the
+    // shared gemv_fused_prologue, same arithmetic, measured slower at one row (qkv
+    // 2560 x 6144 5.40 -> 5.70 us per launch, the 36-layer stack 1107 -> 1121 us), where
+    // it saves little (one scale, few slot divisions).
     const int astride = p.Kp + 16;
     uint8_t* lds_a = smem;
-    if constexpr (FUSED) {
+    if constexpr (FUSED && MR == 1) {
         const bool rne = (p.flags & kFlagRne) != 0;
         float nsc[MR];  // RMSNorm scale per row
 #pragma unroll
@@ -518,9 +794,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             if (!bad_rows) {
                 // finite rows (the usual case): the short rounding sequence
                 if (rne)
-                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows_1<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
                 else
-                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows_1<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
             } else {
 #pragma unroll
                 for (int i = 0; i < XR; ++i) {
@@ -562,6 +838,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                 *reinterpret_cast<uint2*>(lds_a + m * astride + k) = make_uint2(0, 0);
         for (int k = tid * 16; k < p.Kp; k += NT * 16)
             *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
+    } else if constexpr (FUSED) {
+        gemv_fused_prologue<BITS, MODE, NORM, WAVES, MR>(p, xr, gr, sl, nreg, ngroups, smem, astride, s_inv, s_red,
+                                                         s_bad, s_rows);
     }
     lds_barrier();
 
@@ -652,7 +931,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     const int ngroups = p.K >> 3;
     const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    if constexpr (FUSED) {
+    const GemvSlots<FUSED ? XR : 1> sl(gpt);
+    if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
         // weight loads issued after them.
@@ -677,6 +957,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                 }
             }
         }
+    } else if constexpr (FUSED) {
+        gemv_load_rows<MR, XR, NT, NORM>(p, xr, gr, sl, nreg, ngroups);
     } else {
         if (tid < p.M) s_rows[tid] = p.s ? p.s[tid] : 0.0f;
     }
@@ -715,10 +997,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
 
     // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
     // LDS rows 0..M-1 hold the quantized activations; row M is all zeros and feeds
-    // the matrix-core rows M..15.
+    // the matrix-core rows M..15.  One row keeps its prologue written out here: the
+    // shared gemv_fused_prologue, same arithmetic, measured slower at one row (qkv
+    // 2560 x 6144 5.40 -> 5.70 us per launch, the 36-layer stack 1107 -> 1121 us), where
+    // it saves little (one scale, few slot divisions).
     const int astride = p.Kp + 16;
     uint8_t* lds_a = smem;
-    if constexpr (FUSED) {
+    if constexpr (FUSED && MR == 1) {
         const bool rne = (p.flags & kFlagRne) != 0;
         float nsc[MR];  // RMSNorm scale per row
 #pragma unroll
@@ -828,9 +1113,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
             if (!bad_rows) {
                 // finite rows (the usual case): the short rounding sequence
                 if (rne)
-                    gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows_1<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
                 else
-                    gemv_quant_rows<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
+                    gemv_quant_rows_1<BITS, NORM, false, MR>(xr, gr, nsc, inv, lds_a, astride, nreg, gpt, ngroups, tid, NT);
             } else {
 #pragma unroll
                 for (int i = 0; i < XR; ++i) {
@@ -872,6 +1157,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                 *reinterpret_cast<uint2*>(lds_a + m * astride + k) = make_uint2(0, 0);
         for (int k = tid * 16; k < p.Kp; k += NT * 16)
             *reinterpret_cast<uint4*>(lds_a + p.M * astride + k) = make_uint4(0, 0, 0, 0);
+    } else if constexpr (FUSED) {
+        gemv_fused_prologue<BITS, MODE, NORM, WAVES, MR>(p, xr, gr, sl, nreg, ngroups, smem, astride, s_inv, s_red,
+                                                         s_bad, s_rows);
     }
     lds_barrier();
 
@@ -990,7 +1278,11 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
     switch (waves) {
         case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4>(p, grid, items, lds, st);
         case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8>(p, grid, items, lds, st);
-        case 16: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
+        case 16:
+            // several RMSNorm rows do not fit 1024-thread workgroups' registers (gemv_can_fuse
+            // refuses them), so those kernels are not built
+            if constexpr (NORM && MR > 1) return hipErrorInvalidValue;
+            else return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
         default: return hipErrorInvalidValue;  // the LDS above was sized for `waves`
     }
 }
