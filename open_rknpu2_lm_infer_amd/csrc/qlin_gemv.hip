@@ -338,19 +338,13 @@ __device__ __forceinline__ void gemv_load_rows(const GemvParams& p, XGroup<T> (&
 template <int WAVES, int MR>
 __device__ __forceinline__ bool gemv_row_scales(const float (*s_red)[WAVES], const int* s_bad, int M, float (&inv)[MR],
                                                 float* s_rows) {
-    static_assert(MR * WAVES <= 64, "one lane per wave maximum");
     const int lane = threadIdx.x & 63;
-    float am = lane < MR * WAVES ? (&s_red[0][0])[lane] : 0.0f;
     const int bad = lane < WAVES ? s_bad[lane] : 0;
-    am = dpp_max_step<0xB1, 0xf>(am);  // quad_perm [1, 0, 3, 2]
-    am = dpp_max_step<0x4E, 0xf>(am);  // quad_perm [2, 3, 0, 1]: every lane of a quad holds its max
-    if constexpr (WAVES >= 8) am = dpp_max_step<0x141, 0xf>(am);   // row_half_mirror: 8-lane max
-    if constexpr (WAVES >= 16) am = dpp_max_step<0x140, 0xf>(am);  // row_mirror: 16-lane max
+    const float am = rows_max_lanes<WAVES, MR>(&s_red[0][0]);
     const float sc = qscale_from_absmax(am);  // src/npu.rs:1101-1106
     const float iv = 1.0f / sc;
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-        inv[m] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, iv), m * WAVES));
+    for (int m = 0; m < MR; ++m) inv[m] = lane_value(iv, m * WAVES);
     const int row = lane / WAVES;
     if (threadIdx.x < 64 && lane == row * WAVES && row < M && row < MR) s_rows[row] = sc;
     return __ballot(bad) != 0;

@@ -63,4 +63,26 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Per-row maxima of MR rows from per-wave maxima red[m * SEG + w] (SEG waves per row,
+// non-negative values): lane m * SEG + w reads its word and the SEG lanes of each row
+// meet by DPP, so every lane of row m's segment returns row m's max.  One LDS read for
+// all rows instead of MR * SEG broadcast reads in every lane.  The whole wave must be
+// active.
+template <int SEG, int MR>
+__device__ __forceinline__ float rows_max_lanes(const float* red) {
+    static_assert(MR * SEG <= 64 && (SEG == 4 || SEG == 8 || SEG == 16), "segments of 4, 8 or 16 lanes");
+    const int lane = threadIdx.x & 63;
+    float v = lane < MR * SEG ? red[lane] : 0.0f;
+    v = dpp_max_step<0xB1, 0xf>(v);  // quad_perm [1, 0, 3, 2]
+    v = dpp_max_step<0x4E, 0xf>(v);  // quad_perm [2, 3, 0, 1]: every lane of a quad holds its max
+    if constexpr (SEG >= 8) v = dpp_max_step<0x141, 0xf>(v);   // row_half_mirror: 8-lane max
+    if constexpr (SEG >= 16) v = dpp_max_step<0x140, 0xf>(v);  // row_mirror: 16-lane max
+    return v;
+}
+
+// v of lane `src` (a compile-time or wave-uniform lane index).
+__device__ __forceinline__ float lane_value(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
 }  // namespace qlin
