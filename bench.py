@@ -86,6 +86,7 @@ def calibrate(info):
     cal.qcal_stream.argtypes = [P, I64, I, P, P]
     cal.qcal_mfma.argtypes = [I, I, P, P]
     cal.qcal_lds_copy.argtypes = [P, I, I, P, P]
+    cal.qcal_stream_lds.argtypes = [P, I64, I, P, P]
     dev = torch.device("cuda:0")
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -124,7 +125,7 @@ def calibrate(info):
     big = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(1)
     sizes = {n: N * K // 2 + N * 4 for n, K, N in synth.LAYER}
     sizes["sustained_1GiB"] = 1 << 30
-    stream = {}
+    stream, stream_lds = {}, {}
     for name, nb in sizes.items():
         nb = (nb + 4095) // 4096 * 4096
         slots = max(1, (big.numel() - nb) // nb)
@@ -132,8 +133,15 @@ def calibrate(info):
                                                                         sink.data_ptr(), sp()),
                          36 if nb < (1 << 30) else 4)
         stream[name] = {"bytes": nb, "us": round(us, 3), "gbs": round(nb / (us * 1e-6) / 1e9, 1)}
+        # the same bytes as direct global -> LDS copies
+        us = per_call_us(lambda i, nb=nb, slots=slots: cal.qcal_stream_lds(big.data_ptr() + (i % slots) * nb, nb, cus,
+                                                                            sink.data_ptr(), sp()),
+                         36 if nb < (1 << 30) else 4)
+        stream_lds[name] = {"bytes": nb, "us": round(us, 3), "gbs": round(nb / (us * 1e-6) / 1e9, 1)}
     out["stream_floor"] = stream
+    out["stream_floor_lds_copies"] = stream_lds
     log(f"calib: stream floor {stream}")
+    log(f"calib: stream floor, copies into LDS {stream_lds}")
     del big
     # 3. int8 matrix-core rate: 4 workgroups of 4 waves per CU, 4 independent MFMA chains per wave
     iters, grid = 20000, 4 * cus
