@@ -42,6 +42,7 @@
 namespace qlin {
 
 constexpr int kFusedMaxRows = 4;
+constexpr int kGemvRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 word 3)
 
 // Register budget per wave count (1024-thread workgroups get 128 VGPRs per lane):
 // wave steps in flight per register buffer, and 8-element activation groups held
@@ -320,35 +321,42 @@ __device__ __forceinline__ void gemv_load_rows(const GemvParams& p, XGroup<T> (&
         }
     }
     if constexpr (NORM) {
-        // Rows share gamma: row 0's slots (slot j holds group j) load it, the other rows'
-        // slots copy it from there.  One copy per register slot keeps the indexing static;
-        // loading it for every slot issued the same bytes once per row (4 rows: a
-        // quarter of the prologue's load issue time).
+        // Rows share gamma: gr[j] holds the gamma values of this thread's group j, loaded by
+        // row 0's slot j, and every row's slot takes them from there where it is used
+        // (gemv_slot_gamma).  With at least two rows a thread holds at most XR / 2 groups.
+        // Loading gamma for every slot issued the same bytes once per row (4 rows: a
+        // quarter of the prologue's load issue time).  The loads are buffer loads with no
+        // branch: a slot past the row reads beyond the buffer's range, which returns zeros
+        // without a memory access.  (Loaded in branches, the registers were zeroed first
+        // and moved after the loads, which made every wave wait for them before it issued
+        // its first weights.)
+        const __amdgpu_buffer_rsrc_t rg =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.gamma), (short)0, p.K * 4, kGemvRsrcFlags);
 #pragma unroll
-        for (int i = 0; i < XR; ++i) {
-            const int g = tid + NT * sl.j[i];
-            if (i < nreg && g < ngroups) {
-                if (sl.m[i] == 0) {
-                    const float4 a = *reinterpret_cast<const float4*>(p.gamma + 8 * g);
-                    const float4 b = *reinterpret_cast<const float4*>(p.gamma + 8 * g + 4);
-                    gr[i][0] = a.x; gr[i][1] = a.y; gr[i][2] = a.z; gr[i][3] = a.w;
-                    gr[i][4] = b.x; gr[i][5] = b.y; gr[i][6] = b.z; gr[i][7] = b.w;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 1; i < XR; ++i) {
-            const int g = tid + NT * sl.j[i];
-            if (i < nreg && g < ngroups && sl.m[i] != 0) {
-#pragma unroll
-                for (int jj = 0; jj < i; ++jj)  // the row-0 slot of this slot's group (uniform)
-                    if (sl.j[i] == jj) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) gr[i][e] = gr[jj][e];
-                    }
-            }
+        for (int j = 0; j < (XR > 1 ? XR / 2 : 1); ++j) {
+            const int g = tid + NT * j;
+            const int off = sl.m[j] == 0 && g < ngroups ? 32 * g : p.K * 4;
+            const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+            const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16, 0, 0));
+            gr[j][0] = a.x; gr[j][1] = a.y; gr[j][2] = a.z; gr[j][3] = a.w;
+            gr[j][4] = b.x; gr[j][5] = b.y; gr[j][6] = b.z; gr[j][7] = b.w;
         }
     }
+}
+
+// The gamma values of slot i: gr[j[i]], j[i] < XR / 2 (a uniform choice among static
+// registers).
+template <int XR>
+__device__ __forceinline__ void gemv_slot_gamma(const float (&gr)[XR][8], const GemvSlots<XR>& sl, int i,
+                                                float (&gv)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gv[e] = gr[0][e];
+#pragma unroll
+    for (int jj = 1; jj < XR / 2; ++jj)
+        if (sl.j[i] == jj) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) gv[e] = gr[jj][e];
+        }
 }
 
 // Per-token scales from the wave maxima s_red[m][w] and the wave flags s_bad[w]: lane
@@ -502,9 +510,11 @@ __device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const X
                         for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[e]);
                         if constexpr (NORM) {
                             const float ns = row_pick(nsc, m);
+                            float gv[8];
+                            gemv_slot_gamma(gr, sl, i, gv);
 #pragma unroll
                             for (int e = 0; e < 8; ++e) {
-                                v[e] = (v[e] * ns) * gr[i][e];
+                                v[e] = (v[e] * ns) * gv[e];
                                 vn[i][e] = v[e];
                             }
                         }
@@ -551,7 +561,7 @@ __device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const X
                 gemv_quant_vals<false, false, MR>(vn, inv, lds_a, astride, sl, nreg, ngroups, tid, NT, rne);
             }
         } else if (!bad_rows) {
-            // finite rows (the usual case): the short rounding sequence
+            // no RMSNorm: finite rows (the usual case) take the short rounding sequence
             if (rne)
                 gemv_quant_rows<BITS, NORM, true, MR>(xr, gr, nsc, inv, lds_a, astride, sl, nreg, ngroups, tid, NT);
             else
@@ -564,11 +574,6 @@ __device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const X
                     if (g < ngroups) {
                         float v[8];
                         xr[i].get(v);
-                        if constexpr (NORM) {
-                            const float ns = row_pick(nsc, m);
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) v[e] = (v[e] * ns) * gr[i][e];
-                        }
                         const float im = row_pick(inv, m);
                         int q[8];
 #pragma unroll
