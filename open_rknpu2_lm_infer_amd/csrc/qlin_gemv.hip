@@ -37,7 +37,8 @@ int gemv_pick_waves(int groups, int steps) {
 bool gemv_can_fuse(int M, int K, int waves, bool norm) {
     const int nt = 64 * waves;
     const int gpt = (K / 8 + nt - 1) / nt;
-    if (K % 8 || M > kFusedMaxRows || M * gpt > fused_regs(waves, norm)) return false;
+    const int regs = waves >= 16 && !norm && M > 1 ? kWideRowsRegs : fused_regs(waves, norm);
+    if (K % 8 || M > kFusedMaxRows || M * gpt > regs) return false;
     if (norm && (size_t)M * K * 4 > 64 * 1024) return false;  // f32 rows of the RMSNorm in LDS
     // (1024-thread workgroups would spill the per-slot gamma registers)
     if (norm && M > 1 && (waves > 8 || M * gpt > kNormRowsRegs)) return false;

@@ -46,8 +46,8 @@ constexpr int kGemvRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (g
 
 // Register budget per wave count (1024-thread workgroups get 128 VGPRs per lane):
 // wave steps in flight per register buffer, and 8-element activation groups held
-// per thread by the fused prologue.  With RMSNorm each slot also holds its 8 gamma
-// values: 2 slots at 16 waves and 4 below (the f32 rows of the RMSNorm fit 64 KiB of LDS,
+// per thread by the fused prologue.  With RMSNorm a thread also holds 8 gamma values per
+// group: 2 slots at 16 waves and 4 below (the f32 rows of the RMSNorm fit 64 KiB of LDS,
 // K <= 16384, i.e. at most 4 groups per thread at 512 threads), which keeps those
 // kernels from spilling.
 template <int WAVES, bool FUSED>
@@ -57,8 +57,13 @@ struct GemvCfg {
     static constexpr int XREGS_NORM = WAVES >= 16 ? 2 : 4;
 };
 constexpr int fused_regs(int waves, bool norm) { return waves >= 16 ? (norm ? 2 : 4) : (norm ? 4 : 8); }
-// Several rows with RMSNorm hold gamma per register slot as well: fewer slots keep the
-// prologue within the register file.
+// Several rows without RMSNorm in 1024-thread workgroups may hold up to this many groups
+// per thread, in instances of their own (the W8 / W4 down projection, K = 9728, at 3-4
+// rows: 2 groups per row); the 4-slot instances stay for the shorter rows, which ran
+// slower with 8 slots (o at 2 rows 5.01 -> 5.46 us).
+constexpr int kWideRowsRegs = 8;
+// Several rows with RMSNorm: fewer slots keep the prologue (gamma, the normalized values
+// between its two passes) within the register file.
 constexpr int kNormRowsRegs = 4;
 
 // LDS of gemv_items_kernel: the quantized rows (and the f32 rows of the RMSNorm before
@@ -651,14 +656,16 @@ __device__ __forceinline__ void gemv_fetch_params(const GemvParams& p) {
 // MODE 0: q/s given.  MODE 1: fused quant of fp16 rows.  MODE 2: fused quant of f32 rows.
 // MR: largest row count of the fused modes (1 or 4).  NORM: RMSNorm before the
 // quantization (fused modes, one row).
-template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR>
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR, int XW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     using T = typename std::conditional<MODE == 2, float, __half>::type;
     constexpr bool FUSED = MODE != 0;
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM) : GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = XW > 0 ? XW
+                              : NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
+                                     : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -951,14 +958,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
 // Several items per workgroup (fused modes, more items than CUs): the activation
 // prologue as in gemv_kernel, then the flat K-step sequence of the workgroup's items.
-template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR>
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR, int XW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     using T = typename std::conditional<MODE == 2, float, __half>::type;
     constexpr bool FUSED = MODE != 0;
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
-    constexpr int XR = NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM) : GemvCfg<WAVES, FUSED>::XREGS;
+    constexpr int XR = XW > 0 ? XW
+                              : NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
+                                     : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -1274,21 +1283,22 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     }
 }
 
-template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR, int WAVES>
+template <int BITS, bool SWIGLU, int MODE, bool NORM, int MR, int WAVES, int XW = 0>
 static hipError_t launch_k(const GemvParams& p, dim3 grid, bool items, size_t lds, hipStream_t st) {
     if (!items) {
-        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>), grid, dim3(64 * WAVES), lds, st, p);
+        hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR, XW>), grid, dim3(64 * WAVES), lds, st, p);
         return hipGetLastError();
     }
     if constexpr (MODE == 0) {
         return hipErrorInvalidValue;  // several items per workgroup only with fused quantization
     } else {
-        const void* f = reinterpret_cast<const void*>(&gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>);
+        const void* f = reinterpret_cast<const void*>(&gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR, XW>);
         if (lds > 64 * 1024) {
             static const hipError_t a = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
             if (a != hipSuccess) return a;
         }
-        hipLaunchKernelGGL((gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR>), grid, dim3(64 * WAVES), lds, st, p);
+        hipLaunchKernelGGL((gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR, XW>), grid, dim3(64 * WAVES), lds, st,
+                           p);
         return hipGetLastError();
     }
 }
@@ -1304,8 +1314,16 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
         case 16:
             // several RMSNorm rows do not fit 1024-thread workgroups' registers (gemv_can_fuse
             // refuses them), so those kernels are not built
-            if constexpr (NORM && MR > 1) return hipErrorInvalidValue;
-            else return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
+            if constexpr (NORM && MR > 1) {
+                return hipErrorInvalidValue;
+            } else {
+                if constexpr (MR > 1 && MODE != 0) {
+                    const int gpt = ((p.K >> 3) + 1023) / 1024;  // groups per thread per row
+                    if (p.M * gpt > fused_regs(16, false))
+                        return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16, kWideRowsRegs>(p, grid, items, lds, st);
+                }
+                return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16>(p, grid, items, lds, st);
+            }
         default: return hipErrorInvalidValue;  // the LDS above was sized for `waves`
     }
 }

@@ -155,9 +155,9 @@ def test_rmsnorm_rows_fused(oracle, ws, bits, order, M):
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_fused_rows_fewer_waves(oracle, bits, K, M):
     """o / down shapes (N = 2560): 16-wave workgroups hold 4 activation groups of 8 values
-    per thread, so K = 4096 quantizes inside the GEMV up to 4 rows and K = 9728 (two groups
-    per row) up to 2; 3 and 4 rows of K = 9728 fit no wave count and quantize in a separate
-    launch.  Every case equals the separate-quantize launch bit for bit and the oracle."""
+    per thread, so K = 4096 quantizes inside the GEMV up to 4 rows, and 3 and 4 rows of
+    K = 9728 (two groups per row) take the 8-slot instances.  Every case equals the
+    separate-quantize launch bit for bit and the oracle."""
     N = 2560
     ws = ql.Workspace(4, K, N)  # the separate quantization needs room for K columns
     codes = synth.codes(N, K, bits, 330 + bits + K % 11).numpy()
@@ -165,7 +165,7 @@ def test_fused_rows_fewer_waves(oracle, bits, K, M):
     w = make_weights(bits, codes, sc)
     A = synth.activations(M, K, seed=332 + M)
     expect = oracle_linear(oracle, A, codes, sc, False)
-    fused = M <= (4 if K == 4096 else 2)
+    fused = True
     for dt in (torch.float16, torch.float32):
         a = A.to(DEV).to(dt)
         pl = ql.plan(ws, w, a)
