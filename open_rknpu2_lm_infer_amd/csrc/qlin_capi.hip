@@ -573,11 +573,16 @@ GemvPlan plan_gemv(const qlin_workspace* ws, const qlin_weights* w, int rows, bo
         waves = 0;
     }
     g.waves = waves;
-    // More items than CUs with the quantization fused: one workgroup per CU (at most
-    // four items each), so each CU quantizes the rows once.
+    // More items than CUs with the quantization fused: one workgroup per CU (at most four
+    // items each), so each CU quantizes the rows once.  On rows quantized beforehand, only
+    // when one workgroup per item would take a second round of the CUs (1024-thread
+    // workgroups one per CU, smaller ones 16 / waves per CU): 5..16 rows of gate_up 2560 x
+    // 19456, 749 items of 8 waves, 15.5 -> 12.4 us at 8 rows, while qkv 2560 x 6144 (512
+    // items, one round) ran 9.6 -> 10.2 us as 2 items per workgroup.
+    const int per_cu = waves >= 16 || waves <= 0 ? 1 : 16 / waves;
     if (ov.gemv_grid >= 0)
         g.grid = ov.gemv_grid;
-    else if (fused && g.items > ws->cu_count)
+    else if (fused ? g.items > ws->cu_count : g.items > ws->cu_count * per_cu)
         g.grid = std::max(ws->cu_count, (g.items + 3) / 4);
     return g;
 }

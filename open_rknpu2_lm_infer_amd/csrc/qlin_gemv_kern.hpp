@@ -956,8 +956,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
 }
 
-// Several items per workgroup (fused modes, more items than CUs): the activation
-// prologue as in gemv_kernel, then the flat K-step sequence of the workgroup's items.
+// Several items per workgroup (fused modes with more items than CUs, or rows quantized
+// beforehand with more items than one round of workgroups): the activation prologue as
+// in gemv_kernel, then the flat K-step sequence of the workgroup's items.
 template <int BITS, bool SWIGLU, int MODE, bool NORM, int WAVES, int MR, int XW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     using T = typename std::conditional<MODE == 2, float, __half>::type;
@@ -1289,9 +1290,7 @@ static hipError_t launch_k(const GemvParams& p, dim3 grid, bool items, size_t ld
         hipLaunchKernelGGL((gemv_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR, XW>), grid, dim3(64 * WAVES), lds, st, p);
         return hipGetLastError();
     }
-    if constexpr (MODE == 0) {
-        return hipErrorInvalidValue;  // several items per workgroup only with fused quantization
-    } else {
+    {
         const void* f = reinterpret_cast<const void*>(&gemv_items_kernel<BITS, SWIGLU, MODE, NORM, WAVES, MR, XW>);
         if (lds > 64 * 1024) {
             static const hipError_t a = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
