@@ -57,6 +57,9 @@ struct GemvCfg {
     static constexpr int XREGS_NORM = WAVES >= 16 ? 2 : 4;
 };
 constexpr int fused_regs(int waves, bool norm) { return waves >= 16 ? (norm ? 2 : 4) : (norm ? 4 : 8); }
+// Instances for one activation group per thread per row (every multi-row shape but the
+// longest rows): slot i is row i, known at compile time.
+constexpr int kOneGroupRegs = -1;
 // Several rows without RMSNorm in 1024-thread workgroups may hold up to this many groups
 // per thread, in instances of their own (the W8 / W4 down projection, K = 9728, at 3-4
 // rows: 2 groups per row); the 4-slot instances stay for the shorter rows, which ran
@@ -664,8 +667,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
     constexpr int XR = XW > 0 ? XW
-                              : NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
-                                     : GemvCfg<WAVES, FUSED>::XREGS;
+                       : XW < 0 ? MR
+                       : NORM   ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
+                                : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -696,7 +700,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const int ngroups = p.K >> 3;
     const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    const GemvSlots<FUSED ? XR : 1> sl(gpt);
+    // XW < 0: one group per thread per row, so slot i is row i: the slots' rows and
+    // groups are compile-time constants in the unrolled loops and the per-slot row
+    // selects vanish (the multi-row prologue is VALU-bound at 4 rows)
+    const GemvSlots<FUSED ? XR : 1> sl(XW < 0 ? 1 : gpt);
     if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
@@ -967,8 +974,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
     constexpr int XR = XW > 0 ? XW
-                              : NORM ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
-                                     : GemvCfg<WAVES, FUSED>::XREGS;
+                       : XW < 0 ? MR
+                       : NORM   ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
+                                : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_rows[kGemvMaxRows];
@@ -1004,7 +1012,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     const int ngroups = p.K >> 3;
     const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    const GemvSlots<FUSED ? XR : 1> sl(gpt);
+    // XW < 0: one group per thread per row, so slot i is row i: the slots' rows and
+    // groups are compile-time constants in the unrolled loops and the per-slot row
+    // selects vanish (the multi-row prologue is VALU-bound at 4 rows)
+    const GemvSlots<FUSED ? XR : 1> sl(XW < 0 ? 1 : gpt);
     if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
@@ -1307,6 +1318,18 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
     const int groups = gemv_items(p);
     const bool items = p.grid > 0 && p.grid < groups;
     const dim3 grid(items ? p.grid : groups);
+    if constexpr (MR > 1 && MODE != 0) {
+        if ((p.K >> 3) <= 64 * waves) {  // one group per thread per row
+            switch (waves) {
+                case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4, kOneGroupRegs>(p, grid, items, lds, st);
+                case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8, kOneGroupRegs>(p, grid, items, lds, st);
+                case 16:
+                    if constexpr (NORM) return hipErrorInvalidValue;  // as below
+                    else return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16, kOneGroupRegs>(p, grid, items, lds, st);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     switch (waves) {
         case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4>(p, grid, items, lds, st);
         case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8>(p, grid, items, lds, st);
