@@ -9,14 +9,17 @@ namespace qlin {
 // A layer step runs them back to back, and where they sit relative to each other changes
 // its time: the W4 layer (gate_up, qkv, o / down) measured 24.15-24.22 us adjacent, and
 // 24.4 / 24.8 / 25.1 us with 4 / 1 + 5 / 6 + 2 KiB of padding placed between them (same
-// kernels, one box), consistent with the three kernels' code evicting each other from the
-// instruction cache.  Then the RMSNorm and W8 instances of the mixed decode stack.
-template __global__ void gemv_items_kernel<4, true, 1, false, 8, 1, 0>(GemvParams);
-template __global__ void gemv_items_kernel<4, false, 1, false, 8, 1, 0>(GemvParams);
+// kernels, one box), consistent with the kernels' code evicting each other from the
+// instruction cache.  The W4 layer: gate_up, qkv, o (one group per thread), down (two
+// groups per thread); then the RMSNorm and W8 instances of the mixed decode stack.
+template __global__ void gemv_items_kernel<4, true, 1, false, 8, 1, kOneGroupRegs>(GemvParams);
+template __global__ void gemv_items_kernel<4, false, 1, false, 8, 1, kOneGroupRegs>(GemvParams);
+template __global__ void gemv_kernel<4, false, 1, false, 16, 1, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<4, false, 1, false, 16, 1, 0>(GemvParams);
-template __global__ void gemv_items_kernel<4, false, 1, true, 8, 1, 0>(GemvParams);
+template __global__ void gemv_items_kernel<4, false, 1, true, 8, 1, kOneGroupRegs>(GemvParams);
+template __global__ void gemv_kernel<8, false, 1, false, 16, 1, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<8, false, 1, false, 16, 1, 0>(GemvParams);
-template __global__ void gemv_items_kernel<4, true, 1, true, 8, 1, 0>(GemvParams);
+template __global__ void gemv_items_kernel<4, true, 1, true, 8, 1, kOneGroupRegs>(GemvParams);
 
 template <int BITS, bool SWIGLU>
 static hipError_t launch_1row_b(const GemvParams& p, int mode, bool norm, int waves, size_t lds, hipStream_t st) {

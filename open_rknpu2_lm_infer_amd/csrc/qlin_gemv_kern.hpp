@@ -1318,13 +1318,13 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
     const int groups = gemv_items(p);
     const bool items = p.grid > 0 && p.grid < groups;
     const dim3 grid(items ? p.grid : groups);
-    if constexpr (MR > 1 && MODE != 0) {
+    if constexpr (MODE != 0) {
         if ((p.K >> 3) <= 64 * waves) {  // one group per thread per row
             switch (waves) {
                 case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4, kOneGroupRegs>(p, grid, items, lds, st);
                 case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8, kOneGroupRegs>(p, grid, items, lds, st);
                 case 16:
-                    if constexpr (NORM) return hipErrorInvalidValue;  // as below
+                    if constexpr (NORM && MR > 1) return hipErrorInvalidValue;  // as below
                     else return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16, kOneGroupRegs>(p, grid, items, lds, st);
                 default: return hipErrorInvalidValue;
             }
