@@ -7,20 +7,18 @@ namespace qlin {
 // The multi-row decode kernels of a layer, instantiated first and in this order so that
 // each layer's set sits together in the code object whatever else this file instantiates
 // (their layer steps move with where the kernels sit relative to each other): the W4 layer
-// at 2..4 rows (gate_up, qkv, o, down at 2 rows, down at 3..4 rows), then the mixed decode
-// stack's (RMSNorm qkv, W8 o, W8 down at 2 and at 3..4 rows, RMSNorm gate_up).  Measured
+// at 2..4 rows (gate_up, qkv, o, down), then the mixed decode stack's (RMSNorm qkv, W8 o,
+// W8 down, RMSNorm gate_up).  Measured
 // against the compiler's order: W4 layer at 2 / 3 / 4 rows 26.9 / 29.9 / 31.7 -> 26.6 /
 // 29.5 / 31.3 us, the 36-layer stack at 2 / 3 / 4 rows 1260 / 1333 / 1411 -> 1224 / 1308 /
 // 1392 us.
 template __global__ void gemv_items_kernel<4, true, 1, false, 8, 4, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, false, 1, false, 8, 4, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<4, false, 1, false, 16, 4, kOneGroupRegs>(GemvParams);
-template __global__ void gemv_kernel<4, false, 1, false, 16, 4, 0>(GemvParams);
-template __global__ void gemv_kernel<4, false, 1, false, 16, 4, kWideRowsRegs>(GemvParams);
+template __global__ void gemv_kernel<4, false, 1, false, 16, 4, kTwoGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, false, 1, true, 8, 4, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<8, false, 1, false, 16, 4, kOneGroupRegs>(GemvParams);
-template __global__ void gemv_kernel<8, false, 1, false, 16, 4, 0>(GemvParams);
-template __global__ void gemv_kernel<8, false, 1, false, 16, 4, kWideRowsRegs>(GemvParams);
+template __global__ void gemv_kernel<8, false, 1, false, 16, 4, kTwoGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, true, 1, true, 8, 4, kOneGroupRegs>(GemvParams);
 
 size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm, int items) {

@@ -15,10 +15,10 @@ namespace qlin {
 template __global__ void gemv_items_kernel<4, true, 1, false, 8, 1, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, false, 1, false, 8, 1, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<4, false, 1, false, 16, 1, kOneGroupRegs>(GemvParams);
-template __global__ void gemv_kernel<4, false, 1, false, 16, 1, 0>(GemvParams);
+template __global__ void gemv_kernel<4, false, 1, false, 16, 1, kTwoGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, false, 1, true, 8, 1, kOneGroupRegs>(GemvParams);
 template __global__ void gemv_kernel<8, false, 1, false, 16, 1, kOneGroupRegs>(GemvParams);
-template __global__ void gemv_kernel<8, false, 1, false, 16, 1, 0>(GemvParams);
+template __global__ void gemv_kernel<8, false, 1, false, 16, 1, kTwoGroupRegs>(GemvParams);
 template __global__ void gemv_items_kernel<4, true, 1, true, 8, 1, kOneGroupRegs>(GemvParams);
 
 template <int BITS, bool SWIGLU>

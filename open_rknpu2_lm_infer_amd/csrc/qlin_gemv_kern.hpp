@@ -57,13 +57,17 @@ struct GemvCfg {
     static constexpr int XREGS_NORM = WAVES >= 16 ? 2 : 4;
 };
 constexpr int fused_regs(int waves, bool norm) { return waves >= 16 ? (norm ? 2 : 4) : (norm ? 4 : 8); }
-// Instances for one activation group per thread per row (every multi-row shape but the
-// longest rows): slot i is row i, known at compile time.
+// Instances for one (or two) activation groups per thread per row, known at compile time:
+// slot i holds group i % gpt of row i / gpt, so the slots' rows and groups are constants in
+// the unrolled prologue loops.  One group: every shape but the longest rows; two: the down
+// projection (K = 9728) at 16 waves.
 constexpr int kOneGroupRegs = -1;
+constexpr int kTwoGroupRegs = -2;
 // Several rows without RMSNorm in 1024-thread workgroups may hold up to this many groups
-// per thread, in instances of their own (the W8 / W4 down projection, K = 9728, at 3-4
-// rows: 2 groups per row); the 4-slot instances stay for the shorter rows, which ran
-// slower with 8 slots (o at 2 rows 5.01 -> 5.46 us).
+// per thread, in instances of their own (rows of 3-4 groups per thread at 2 rows; the
+// down projection, K = 9728, two groups per row, takes the two-group instances above);
+// the 4-slot instances stay for the shorter rows, which ran slower with 8 slots (o at 2
+// rows 5.01 -> 5.46 us).
 constexpr int kWideRowsRegs = 8;
 // Several rows with RMSNorm: fewer slots keep the prologue (gamma, the normalized values
 // between its two passes) within the register file.
@@ -667,7 +671,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
     constexpr int XR = XW > 0 ? XW
-                       : XW < 0 ? MR
+                       : XW < 0 ? MR * -XW
                        : NORM   ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
                                 : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
@@ -698,12 +702,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     XGroup<T> xr[FUSED ? XR : 1];
     float gr[NORM ? XR : 1][8];
     const int ngroups = p.K >> 3;
-    const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
+    const int gpt = XW < 0 ? -XW : (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    // XW < 0: one group per thread per row, so slot i is row i: the slots' rows and
-    // groups are compile-time constants in the unrolled loops and the per-slot row
-    // selects vanish (the multi-row prologue is VALU-bound at 4 rows)
-    const GemvSlots<FUSED ? XR : 1> sl(XW < 0 ? 1 : gpt);
+    // XW < 0: -XW groups per thread per row, known at compile time, so the slots' rows
+    // and groups are constants in the unrolled loops and the per-slot row selects vanish
+    // (the multi-row prologue is VALU-bound at 4 rows)
+    const GemvSlots<FUSED ? XR : 1> sl(gpt);
     if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
@@ -974,7 +978,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr int KS = BITS == 4 ? 256 : 128;
     constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
     constexpr int XR = XW > 0 ? XW
-                       : XW < 0 ? MR
+                       : XW < 0 ? MR * -XW
                        : NORM   ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
                                 : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
@@ -1010,12 +1014,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     XGroup<T> xr[FUSED ? XR : 1];
     float gr[NORM ? XR : 1][8];
     const int ngroups = p.K >> 3;
-    const int gpt = (ngroups + NT - 1) / NT;  // groups per thread per row
+    const int gpt = XW < 0 ? -XW : (ngroups + NT - 1) / NT;  // groups per thread per row
     const int nreg = FUSED ? p.M * gpt : 0;   // uniform
-    // XW < 0: one group per thread per row, so slot i is row i: the slots' rows and
-    // groups are compile-time constants in the unrolled loops and the per-slot row
-    // selects vanish (the multi-row prologue is VALU-bound at 4 rows)
-    const GemvSlots<FUSED ? XR : 1> sl(XW < 0 ? 1 : gpt);
+    // XW < 0: -XW groups per thread per row, known at compile time, so the slots' rows
+    // and groups are constants in the unrolled loops and the per-slot row selects vanish
+    // (the multi-row prologue is VALU-bound at 4 rows)
+    const GemvSlots<FUSED ? XR : 1> sl(gpt);
     if constexpr (FUSED && MR == 1) {
         // Only owned groups are loaded.  These loads may sit in branches because every
         // weight load below is unconditional: waits for them then count exactly the
@@ -1319,7 +1323,12 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
     const bool items = p.grid > 0 && p.grid < groups;
     const dim3 grid(items ? p.grid : groups);
     if constexpr (MODE != 0) {
-        if ((p.K >> 3) <= 64 * waves) {  // one group per thread per row
+        const int gpt = ((p.K >> 3) + 64 * waves - 1) / (64 * waves);  // groups per thread per row
+        if constexpr (!NORM) {
+            if (gpt == 2 && waves == 16)
+                return launch_k<BITS, SWIGLU, MODE, NORM, MR, 16, kTwoGroupRegs>(p, grid, items, lds, st);
+        }
+        if (gpt == 1) {
             switch (waves) {
                 case 4: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 4, kOneGroupRegs>(p, grid, items, lds, st);
                 case 8: return launch_k<BITS, SWIGLU, MODE, NORM, MR, 8, kOneGroupRegs>(p, grid, items, lds, st);
