@@ -179,3 +179,29 @@ def test_fused_rows_fewer_waves(oracle, bits, K, M):
     w.close()
     ws.close()
 
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2])
+def test_fused_rows_three_groups_per_thread(oracle, bits, M):
+    """K = 20480 at 16 waves: three activation groups of each row per thread, the slot
+    layout chosen at run time (8-slot instances at two rows; one and two groups per thread
+    take instances with the layout fixed at compile time).  Equal to the separate-quantize
+    launch bit for bit and to the oracle."""
+    K, N = 20480, 512
+    ws = ql.Workspace(2, K, N)
+    codes = synth.codes(N, K, bits, 340 + bits).numpy()
+    sc = synth.scales(N, bits, 341 + bits).numpy()
+    w = make_weights(bits, codes, sc)
+    A = synth.activations(M, K, seed=342 + M)
+    expect = oracle_linear(oracle, A, codes, sc, False)
+    a = A.to(DEV).to(torch.float16)
+    pl = ql.plan(ws, w, a)
+    assert pl["path"] == ql.QLIN_PATH_GEMV_FUSED and pl["waves"] == 16, pl
+    out = ql.run(ws, w, a, out_dtype=torch.float16)
+    sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=ql.QLIN_NO_FUSED_QUANT)
+    torch.cuda.synchronize()
+    assert np.array_equal(f16_bits(out), f16_bits(sep))
+    check_outputs(oracle, out, expect, False, torch.float16)
+    w.close()
+    ws.close()
