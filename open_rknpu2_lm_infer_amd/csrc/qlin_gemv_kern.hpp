@@ -1074,8 +1074,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     // PRE batches in flight during the prologue: two with up to 8 waves; one with 16,
     // whose 1024 threads already fill the CU's queue, and one with SwiGLU, whose steps
     // load twice the bytes (two batches there delayed the prologue: gate_up 2560x19456
-    // 9.55 -> 8.89 us with one).  Unconditional, so that the waits for the activation
-    // loads above count exactly these loads after them.
+    // 9.55 -> 8.89 us with one; with one activation group per thread 8.45 against 8.02
+    // us).  Unconditional, so that the waits for the activation loads above count
+    // exactly these loads after them.
     constexpr int PRE = WAVES <= 8 && !SWIGLU ? 2 : 1;
     load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
     if constexpr (PRE == 2) {
