@@ -267,13 +267,17 @@ int qlin_run_plan(const qlin_workspace* ws, const qlin_weights* weights, int32_t
 /* ---- kernel-variant selection ----
  * Replaces the NPU strategy search and its on-disk cache (src/npu.rs:595-996, driven by
  * src/cli/tune.rs:10-59).  qlin_tune times, on `stream`, the variants of the path a run of
- * `rows` rows takes (decode GEMV: 4, 8 or 16 waves per channel group; GEMM: 1..8 k splits),
+ * `rows` rows takes (decode GEMV: 4, 8 or 16 waves per channel group; GEMM: the 16x16x64
+ * kernel and each tile configuration of the 32x32x32 kernel, each with 1..8 k splits),
  * checks that they all produce the same output, and records the fastest for the key (bits,
  * K, N, rows bucket, path, QLIN_SWIGLU); later runs with that key use it.  The table is
- * process-wide (all devices; tune on the device that runs).  QLIN_GEMV_WAVES and
- * QLIN_GEMM_SPLITS in the environment still take precedence.  flags: 0 or QLIN_SWIGLU.
- * qlin_tune_load returns the number of entries read (or an error code); the file is text,
- * one entry per line. */
+ * process-wide (all devices; tune on the device that runs).  QLIN_GEMV_WAVES,
+ * QLIN_GEMM_SPLITS, QLIN_GEMM_KERNEL and QLIN_GEMM_CFG in the environment still take
+ * precedence.  flags: 0 or QLIN_SWIGLU.  qlin_tune_load returns the number of entries read
+ * (or an error code); the file is text, one entry per line: bits K N rows_bucket path swiglu
+ * variant, the variant being the GEMV's waves (4, 8, 16) or, for a GEMM (path 2), splits +
+ * 100 * kernel with splits 1..64 and kernel 0 (the planner's pick), 1 (16x16x64) or 2 + c
+ * (32x32x32 in tile configuration c = 0..3; c = 3 for W4 only). */
 int qlin_tune(qlin_workspace* ws, const qlin_weights* weights, int32_t rows, uint32_t flags, int32_t reps,
               void* stream);
 int qlin_tune_count(void);

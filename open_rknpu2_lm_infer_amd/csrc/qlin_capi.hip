@@ -93,8 +93,12 @@ int current_device(int* dev) { return hipGetDevice(dev) == hipSuccess ? QLIN_OK 
 
 // ---- kernel-variant table (qlin_tune) ------------------------------------------------
 // Key: bits, K, N, rows bucket, path (0 decode GEMV with fused quantization, 1 decode GEMV
-// from quantized rows, 2 GEMM), SwiGLU.  Value: GEMV waves per group or GEMM k splits.
+// from quantized rows, 2 GEMM), SwiGLU.  Value: GEMV waves per group, or for a GEMM
+// k splits + kTuneKernelStep * kernel, kernel 0 the planner's own pick, 1 the 16x16x64
+// kernel, 2 + c the 32x32x32 kernel in tile configuration c (0..3; 3 for W4 only).
 using TuneKey = std::tuple<int, int, int, int, int, int>;
+constexpr int kTuneKernelStep = 100, kTuneMaxSplits = 64;
+constexpr int kTuneKernel16 = 1, kTuneKernel32 = 2;
 std::map<TuneKey, int>& tune_table() {
     static std::map<TuneKey, int> t;
     return t;
@@ -646,10 +650,14 @@ struct GemmPlan {
 // every CU several tiles (M = 4096 gate_up: 194-206 vs 212-227 us); with one round or less
 // the 16x16x64 kernel is equal or ahead (M = 512: the 128 x 128 tiles of both run at the
 // same copy rate, ~20 B per clock per CU), so it stays the default there.
-// Returns -1 for the 16x16x64 kernel, else the 32x32x32 tile configuration.
-int gemm_pick(const qlin_workspace* ws, const qlin_weights* w, int rows, bool sw) {
+// Returns -1 for the 16x16x64 kernel, else the 32x32x32 tile configuration.  `tuned` is the
+// kernel field of a variant-table entry (0: none), below the environment overrides.
+int gemm_pick(const qlin_workspace* ws, const qlin_weights* w, int rows, bool sw, int tuned) {
     if (ws->ov.gemm_kernel == 16) return -1;
     if (ws->ov.gemm_cfg >= 0 && ws->ov.gemm_cfg <= 3) return ws->ov.gemm_cfg == 3 && w->bits != 4 ? -1 : ws->ov.gemm_cfg;
+    if (tuned == kTuneKernel16) return -1;
+    if (tuned >= kTuneKernel32 && tuned <= kTuneKernel32 + 3)
+        return tuned == kTuneKernel32 + 3 && w->bits != 4 ? -1 : tuned - kTuneKernel32;
     if (w->bits != 4) return -1;
     const GemmTileCfg big = gemm32_tile(w->bits, 1);
     const int cols = sw ? w->N / 2 : w->N, bcols = sw ? big.bn / 2 : big.bn;
@@ -671,7 +679,8 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
     const QlinOverrides& ov = ws->ov;
     const bool sw = (flags & kFlagSwiglu) != 0;
     GemmPlan g{};
-    const int pick = gemm_pick(ws, w, rows, sw);
+    const int tuned = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);  // splits + step * kernel
+    const int pick = gemm_pick(ws, w, rows, sw, tuned / kTuneKernelStep);
     g.kernel = pick < 0 ? 16 : 32;
     int64_t slice;  // ints of one partial tile
     if (g.kernel == 32) {
@@ -694,7 +703,7 @@ int plan_gemm(const qlin_workspace* ws, const qlin_weights* w, int rows, uint32_
     const int ktiles = w->Kp / kGemmTileK;
     const int tiles = g.m_tiles * g.n_tiles;
     int S = ov.gemm_splits;
-    if (S <= 0) S = tuned_variant(w->bits, w->K, w->N, rows, 2, sw);
+    if (S <= 0) S = tuned % kTuneKernelStep;
     if (S <= 0) {
         // Split K while the grid stays within one workgroup per CU (split-K's partial round
         // trip costs more than a second resident workgroup per CU gains), keeping >= 4 k
@@ -981,6 +990,18 @@ static_assert(kNaPartOff % 256 == 0 && kNaQOff % 256 == 0, "scratch regions stay
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
+
+// Input of a variant search: fp16 values in [-2, 2) from a hash of the index.
+__global__ void tune_fill_kernel(_Float16* a, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        uint32_t h = (uint32_t)i * 2654435761u;
+        h ^= h >> 15;
+        h *= 2246822519u;
+        h ^= h >> 13;
+        a[i] = (_Float16)((float)(h & 0xffffu) * (4.0f / 65536.0f) - 2.0f);
+    }
+}
 
 __global__ void zero_words_kernel(uint32_t* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
@@ -1283,7 +1304,11 @@ int qlin_tune(qlin_workspace* ws, const qlin_weights* w, int32_t rows, uint32_t 
         (void)hipFree(A);
         return QLIN_ERR_NOMEM;
     }
-    int rc = hipMemset(A, 0x3c, a_bytes) == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;  // every value 1.0 (0x3c3c)
+    // varied input values rather than a constant, so the timed kernels see data like real
+    // activations
+    const int64_t na = (int64_t)rows * w->K;
+    tune_fill_kernel<<<(unsigned)((na + 255) / 256), 256, 0, st>>>(A, na);
+    int rc = hipGetLastError() == hipSuccess ? QLIN_OK : QLIN_ERR_DEVICE;
     const bool fused = gemv_fusable(ws, w, rows, A, w->K, nullptr, flags);
     const int path = fused ? 0 : (gemv_ok(ws, w, rows) ? 1 : 2);
     std::vector<int> cand;
@@ -1291,33 +1316,46 @@ int qlin_tune(qlin_workspace* ws, const qlin_weights* w, int32_t rows, uint32_t 
         for (int v : {4, 8, 16})
             if (!fused || gemv_can_fuse(rows, w->K, v, false)) cand.push_back(v);
     } else {
+        // every kernel and tile configuration with 1..8 k splits (the planner trims a split
+        // count that its partial buffer or counters cannot hold)
         const int ktiles = w->Kp / kGemmTileK;
-        for (int v : {1, 2, 3, 4, 6, 8})
-            if (2 * v <= ktiles) cand.push_back(v);
+        for (int kern = kTuneKernel16; kern <= kTuneKernel32 + 3; ++kern) {
+            if (kern == kTuneKernel32 + 3 && w->bits != 4) continue;  // 256 x 192 tiles: W4 only
+            for (int v : {1, 2, 3, 4, 6, 8})
+                if (2 * v <= ktiles) cand.push_back(v + kTuneKernelStep * kern);
+        }
     }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)) rc = QLIN_ERR_DEVICE;
     std::vector<uint16_t> ref(c_bytes / 2), got(c_bytes / 2);
-    float best_ms = 0.0f;
-    int best = 0;
-    for (size_t i = 0; i < cand.size() && !rc; ++i) {
-        g_force_variant = cand[i];
-        rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);  // warm-up
-        if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = QLIN_ERR_DEVICE;
-        for (int r = 0; r < reps && !rc; ++r)
-            rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);
-        float ms = 0.0f;
-        if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
-                    hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
-            rc = QLIN_ERR_DEVICE;
-        // every variant computes the same integers and epilogue: the outputs must agree
-        if (!rc && hipMemcpy((i == 0 ? ref : got).data(), C, c_bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = QLIN_ERR_DEVICE;
-        if (!rc && i > 0 && std::memcmp(ref.data(), got.data(), c_bytes) != 0) rc = QLIN_ERR_DEVICE;
-        if (!rc && (best == 0 || ms < best_ms)) {
-            best_ms = ms;
-            best = cand[i];
+    // two passes over the candidates, each timed after a warm-up run, the faster pass
+    // counting: a candidate's time does not depend on where in the sequence it ran
+    std::vector<float> ms_min(cand.size(), 0.0f);
+    for (int pass = 0; pass < 2 && !rc; ++pass) {
+        for (size_t i = 0; i < cand.size() && !rc; ++i) {
+            g_force_variant = cand[i];
+            rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);  // warm-up
+            if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = QLIN_ERR_DEVICE;
+            for (int r = 0; r < reps && !rc; ++r)
+                rc = run_impl(ws, w, rows, A, QLIN_F16, w->K, nullptr, 0.0f, C, QLIN_F16, ncols, flags, st);
+            float ms = 0.0f;
+            if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                        hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+                rc = QLIN_ERR_DEVICE;
+            // every variant computes the same integers and epilogue: the outputs must agree
+            if (!rc && pass == 0) {
+                if (hipMemcpy((i == 0 ? ref : got).data(), C, c_bytes, hipMemcpyDeviceToHost) != hipSuccess)
+                    rc = QLIN_ERR_DEVICE;
+                else if (i > 0 && std::memcmp(ref.data(), got.data(), c_bytes) != 0)
+                    rc = QLIN_ERR_DEVICE;
+            }
+            if (!rc && (pass == 0 || ms < ms_min[i])) ms_min[i] = ms;
         }
     }
+    size_t bi = 0;
+    for (size_t i = 1; i < cand.size(); ++i)
+        if (ms_min[i] < ms_min[bi]) bi = i;
+    const int best = rc || cand.empty() ? 0 : cand[bi];
     g_force_variant = 0;
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
@@ -1363,10 +1401,14 @@ int qlin_tune_load(const char* path) {
     std::lock_guard<std::mutex> g(tune_mutex());
     while (std::fgets(line, sizeof line, f)) {
         if (line[0] == '#' || line[0] == '\n') continue;
-        int b, K, N, r, path_, swg, v;
-        if (std::sscanf(line, "%d %d %d %d %d %d %d", &b, &K, &N, &r, &path_, &swg, &v) != 7 || (b != 4 && b != 8) ||
-            K <= 0 || N <= 0 || r <= 0 || path_ < 0 || path_ > 2 || (swg != 0 && swg != 1) || v <= 0 ||
-            (path_ < 2 && v != 4 && v != 8 && v != 16)) {
+        int b = 0, K = 0, N = 0, r = 0, path_ = -1, swg = -1, v = 0;
+        const bool parsed = std::sscanf(line, "%d %d %d %d %d %d %d", &b, &K, &N, &r, &path_, &swg, &v) == 7;
+        // a GEMM entry: 1..64 splits and a kernel field of 0..5 (5, the 256 x 192 tiles, W4 only)
+        const bool ok_gemm = v % kTuneKernelStep >= 1 && v % kTuneKernelStep <= kTuneMaxSplits &&
+                             v / kTuneKernelStep <= kTuneKernel32 + (b == 4 ? 3 : 2);
+        if (!parsed || (b != 4 && b != 8) || K <= 0 || N <= 0 || r <= 0 || path_ < 0 || path_ > 2 ||
+            (swg != 0 && swg != 1) || v <= 0 || (path_ < 2 && v != 4 && v != 8 && v != 16) ||
+            (path_ == 2 && !ok_gemm)) {
             rc = QLIN_ERR_PARAM;
             break;
         }

@@ -5,9 +5,11 @@ C ABI, against the CPU oracle.
   N(0,1) activations with 1% x20 outlier channels (src/npu.rs:1052-1062, the W8 dynamic
   path), in both rounding modes and through the synchronous host entry point.
 - One W4 layer at M=4096 with Student-t(3) activations: RMSNorm fused into the
-  quantization of qkv and gate_up, SiLU-gate epilogue on gate_up.  q and s on every row,
-  int32 sums and fp16 outputs on two rows of every 128-row tile over all channels, and
-  the whole output free of NaN.
+  quantization of qkv and gate_up, SiLU-gate epilogue on gate_up.  q and s on every row;
+  int32 sums and fp16 outputs against the oracle on two rows of every 128-row tile over
+  all channels; every row's int32 sums against the platform's int8 GEMM (torch._int_mm,
+  exact integer arithmetic) on the same q and codes, and every output against the
+  oracle's dequant of those sums; the whole output free of NaN.
 - The 36-layer mixed W4/W8 decoder stack at M=1 and M=4 (src/model/dense.rs:398-540:
   RMSNorm -> qkv -> o (+ residual) -> RMSNorm -> gate_up + SiLU-gate -> down
   (+ residual)), run as one launch per linear and as the one-launch decode chain; every
@@ -104,9 +106,9 @@ def test_long_prefill_m4096(oracle, ws4096, p):
     name, K, N = synth.LAYER[p]
     swiglu = name == "gate_up"
     say(f"M=4096 {name} {K}x{N}")
-    packed, codes, sc = synth.make_linear(N, K, 4, synth.linear_seed(0, p), device=DEV)
+    packed, codes_d, sc = synth.make_linear(N, K, 4, synth.linear_seed(0, p), device=DEV)
     w = ql.Weights.from_packed_device(4, K, N, packed, sc)
-    codes, sc = host(codes), host(sc)
+    codes, sc = host(codes_d), host(sc)
     del packed
     A = synth.activations(M, K, seed=50100 + p, device=DEV, dist="student_t3")
     gamma = synth.gamma(K, seed=50000 + p // 2, device=DEV) if name in ("qkv", "gate_up") else None
@@ -135,12 +137,26 @@ def test_long_prefill_m4096(oracle, ws4096, p):
     got = host(acc[torch.as_tensor(rows, device=DEV)])
     bad = np.argwhere(got != acc_ref)
     assert len(bad) == 0, f"{len(bad)} int32 mismatches, first {bad[:3].tolist()}"
-    del acc
     ref = oracle.dequant(acc_ref, s_ref[rows], sc)
     if swiglu:
         ref = oracle.swiglu(ref)
     check_outputs(oracle, out[torch.as_tensor(rows, device=DEV)], ref, swiglu, torch.float16)
     assert not torch.isnan(out).any()
+
+    # every row: the int32 sums against the platform's int8 GEMM (torch._int_mm, exact
+    # integer products and sums) on the same q and codes, then every output against the
+    # oracle's dequant (+ SiLU-gate) of those sums
+    blas = torch._int_mm(q[:, :K].contiguous(), codes_d.t())
+    torch.cuda.synchronize()
+    assert torch.equal(acc, blas), f"{int((acc != blas).sum())} int32 mismatches against torch._int_mm"
+    del blas, codes_d
+    acc_all = host(acc)
+    del acc
+    ref = oracle.dequant(acc_all, s_ref, sc)
+    del acc_all
+    if swiglu:
+        ref = oracle.swiglu(ref)
+    check_outputs(oracle, out, ref, swiglu, torch.float16)
     w.close()
 
 
