@@ -34,7 +34,7 @@ struct QlinOverrides {
     int gemv_item_width;  // QLIN_GEMV_ITEM_WIDTH, 1..16
     int gemv_waves;       // QLIN_GEMV_WAVES, 4 / 8 / 16
     int gemv_grid;        // QLIN_GEMV_GRID, >= 0 (0: one workgroup per item)
-    int fused_max_rows;   // QLIN_FUSED_QUANT_MAX_ROWS (default 4)
+    int fused_max_rows;   // QLIN_FUSED_QUANT_MAX_ROWS (default 8)
     int gemm_splits;      // QLIN_GEMM_SPLITS
     int gemm_target_wgs;  // QLIN_GEMM_TARGET_WGS (default: the CU count)
     int gemm_group_m;     // QLIN_GEMM_GROUP_M (default 4)
@@ -78,7 +78,7 @@ QlinOverrides read_overrides() {
     o.gemv_item_width = env_int("QLIN_GEMV_ITEM_WIDTH", 0);
     o.gemv_waves = env_int("QLIN_GEMV_WAVES", 0);
     o.gemv_grid = env_int("QLIN_GEMV_GRID", -1);
-    o.fused_max_rows = env_int("QLIN_FUSED_QUANT_MAX_ROWS", 4);
+    o.fused_max_rows = env_int("QLIN_FUSED_QUANT_MAX_ROWS", kFusedMaxRows);
     o.gemm_splits = env_int("QLIN_GEMM_SPLITS", 0);
     o.gemm_target_wgs = env_int("QLIN_GEMM_TARGET_WGS", 0);
     o.gemm_group_m = env_int("QLIN_GEMM_GROUP_M", 4);
@@ -543,6 +543,7 @@ struct ResidualArgs {
 // K = 4096 3 rows 6.94 vs 7.38, 4 rows 7.79 vs 7.50 (every workgroup re-reads and
 // quantizes all rows, so 4 rows keep the separate launch); K = 9728 2 rows 10.99 vs 10.96.
 int gemv_fused_waves(int rows, int K, int groups, int steps, bool norm) {
+    if (rows > kFusedRowsWide) return gemv_can_fuse(rows, K, 8, norm) ? 8 : 0;  // the 8-row instances
     for (int w = gemv_pick_waves(groups, steps); w >= 4; w /= 2) {
         if (gemv_can_fuse(rows, K, w, norm)) return w;
         if (rows >= 4) break;

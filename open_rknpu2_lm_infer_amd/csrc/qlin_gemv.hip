@@ -28,7 +28,7 @@ size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm
         if (norm) a = std::max(a, (size_t)M * K * sizeof(float));
         return std::max(a, (size_t)2 * waves * 64 * 4 * sizeof(int));
     }
-    const size_t rows = fused ? (M == 1 ? 1 : 4) : kGemvMaxRows;  // rows leaving the matrix core
+    const size_t rows = fused ? (M == 1 ? 1 : M <= kFusedRowsWide ? 4 : 8) : kGemvMaxRows;  // rows leaving the matrix core
     const size_t live = 16 * ((rows + 3) / 4), regs = rows < 4 ? rows : 4;
     const size_t red = (size_t)items * 2 * waves * live * regs * sizeof(int);
     return gemv_red_offset(M, Kp, K, fused, norm) + red;
@@ -56,6 +56,8 @@ bool gemv_can_fuse(int M, int K, int waves, bool norm) {
     const int gpt = (K / 8 + nt - 1) / nt;
     const int regs = waves >= 16 && !norm && M > 1 ? kWideRowsRegs : fused_regs(waves, norm);
     if (K % 8 || M > kFusedMaxRows || M * gpt > regs) return false;
+    // 5..8 rows: the 8-row instances only (8 waves, one group per thread per row, no RMSNorm)
+    if (M > kFusedRowsWide && (norm || waves != 8 || gpt != 1)) return false;
     if (norm && (size_t)M * K * 4 > 64 * 1024) return false;  // f32 rows of the RMSNorm in LDS
     // (1024-thread workgroups would spill the per-slot gamma registers)
     if (norm && M > 1 && (waves > 8 || M * gpt > kNormRowsRegs)) return false;
@@ -66,6 +68,7 @@ template <int BITS, bool SWIGLU, int MODE>
 static hipError_t launch_m(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
     const bool norm = p.gamma != nullptr;  // fused RMSNorm
     if (p.M == 1) return launch_gemv_1row(p, BITS, SWIGLU, MODE, norm, waves, lds, st);
+    if (p.M > kFusedRowsWide) return norm ? hipErrorInvalidValue : launch_gemv_8rows(p, BITS, SWIGLU, MODE, waves, lds, st);
     return norm ? launch_w<BITS, SWIGLU, MODE, true, 4>(p, waves, lds, st)
                 : launch_w<BITS, SWIGLU, MODE, false, 4>(p, waves, lds, st);
 }

@@ -41,7 +41,6 @@
 
 namespace qlin {
 
-constexpr int kFusedMaxRows = 4;
 constexpr int kGemvRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 word 3)
 
 // Register budget per wave count (1024-thread workgroups get 128 VGPRs per lane):
@@ -514,7 +513,7 @@ __device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const X
                         const uint4 r = xr[i].raw;
                         const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
                         bad |= mb > 0x7bffu;
-                        lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                        lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);  // Inf / NaN: folded again below
                     } else {
                         float v[8];
                         xr[i].get(v);
@@ -538,6 +537,26 @@ __device__ __forceinline__ void gemv_fused_prologue(const GemvParams& p, const X
 #pragma unroll
                     for (int mm = 0; mm < MR; ++mm)
                         if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
+                }
+            }
+        }
+        if constexpr (MODE == 1 && !NORM) {
+            // A group holding Inf or NaN (rare) was left out of the maxima above: fold them
+            // again as the reference does.  Wave-uniform: with several rows per thread the
+            // branch-free fold of the one-row kernels costs more VALU in every launch.
+            if (__builtin_expect(__ballot(bad) != 0, 0)) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < XR; ++i) {
+                    const int m = sl.m[i], g = tid + NT * sl.j[i];
+                    if (i < nreg && g < ngroups) {
+                        bool nonfinite;
+                        const float lm = f32_of_f16_bits(absmax_bits_f16x8_ref(xr[i].raw, nonfinite));
+#pragma unroll
+                        for (int mm = 0; mm < MR; ++mm)
+                            if (mm == m) mx[mm] = fmaxf(mx[mm], lm);
+                    }
                 }
             }
         }
@@ -811,9 +830,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
                         if constexpr (MODE == 1 && !NORM) {
                             // fp16 rows: absmax and finiteness from the bit patterns
                             const uint4 r = xr[i].raw;
-                            const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
-                            bad |= mb > 0x7bffu;
-                            lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                            bool nonfinite;
+                            const uint32_t mb = absmax_bits_f16x8_ref(r, nonfinite);
+                            bad |= nonfinite;
+                            lm = f32_of_f16_bits(mb);
                         } else {
                             float v[8];
                             xr[i].get(v);
@@ -1138,9 +1158,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
                         if constexpr (MODE == 1 && !NORM) {
                             // fp16 rows: absmax and finiteness from the bit patterns
                             const uint4 r = xr[i].raw;
-                            const uint32_t mb = absmax_bits_f16x8(r.x, r.y, r.z, r.w);
-                            bad |= mb > 0x7bffu;
-                            lm = f32_of_f16_bits(mb > 0x7bffu ? 0u : mb);
+                            bool nonfinite;
+                            const uint32_t mb = absmax_bits_f16x8_ref(r, nonfinite);
+                            bad |= nonfinite;
+                            lm = f32_of_f16_bits(mb);
                         } else {
                             float v[8];
                             xr[i].get(v);
@@ -1366,5 +1387,10 @@ static hipError_t launch_w(const GemvParams& p, int waves, size_t lds, hipStream
 // instruction for instruction the same and differed only in where they were placed.
 hipError_t launch_gemv_1row(const GemvParams& p, int bits, bool swiglu, int mode, bool norm, int waves, size_t lds,
                             hipStream_t st);
+
+// 5..8-row instances (qlin_gemv_8rows.hip): 8 waves, one activation group per thread per
+// row, no RMSNorm.
+hipError_t launch_gemv_8rows(const GemvParams& p, int bits, bool swiglu, int mode, int waves, size_t lds,
+                             hipStream_t st);
 
 }  // namespace qlin

@@ -20,6 +20,10 @@ constexpr int kKAlign = 256;  // Kp alignment (one GEMV wave step of W4 spans 25
 constexpr int kNAlign = 64;   // Np alignment
 constexpr int kMaxK = 131072; // int32 accumulators cannot overflow below this K (W4 codes x16)
 constexpr int kGemvMaxRows = 16;
+// Rows a fused GEMV prologue quantizes: up to 4 in every instance, 5..8 in the 8-row
+// instances (512-thread workgroups, one activation group per thread per row, no RMSNorm).
+constexpr int kFusedMaxRows = 8;
+constexpr int kFusedRowsWide = 4;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -183,6 +187,28 @@ __device__ __forceinline__ uint32_t absmax_bits_f16x8(uint32_t a, uint32_t b, ui
 }
 __device__ __forceinline__ float f32_of_f16_bits(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+// Largest |x| of eight fp16 values (one 16-byte group) as the reference folds them
+// (f32::max over |x|, src/npu.rs:1101-1106: NaN ignored, Inf kept), as an fp16 bit pattern,
+// and whether any of them is Inf or NaN.  Each sign-masked pattern h is taken as the signed
+// 16-bit value h + 0x3ff: finite values and Inf keep their order at 0x3ff..0x7fff, and NaN
+// patterns (h > 0x7c00) wrap below zero, so one signed max passes over them.  A group of
+// eight NaN gives 0.
+__device__ __forceinline__ uint32_t absmax_bits_f16x8_ref(uint4 r, bool& nonfinite) {
+    typedef short i16x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 off = {0x3ff, 0x3ff};
+    const i16x2 b0 = __builtin_bit_cast(i16x2, __builtin_bit_cast(u16x2, r.x & 0x7fff7fffu) + off);
+    const i16x2 b1 = __builtin_bit_cast(i16x2, __builtin_bit_cast(u16x2, r.y & 0x7fff7fffu) + off);
+    const i16x2 b2 = __builtin_bit_cast(i16x2, __builtin_bit_cast(u16x2, r.z & 0x7fff7fffu) + off);
+    const i16x2 b3 = __builtin_bit_cast(i16x2, __builtin_bit_cast(u16x2, r.w & 0x7fff7fffu) + off);
+    const i16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(b0, b1), __builtin_elementwise_max(b2, b3));
+    const int top = m.x > m.y ? m.x : m.y;
+    // a NaN wrapped below zero (sign bit set); an Inf is the top value 0x7c00 + 0x3ff
+    const uint32_t signs = (__builtin_bit_cast(uint32_t, b0) | __builtin_bit_cast(uint32_t, b1) |
+                            __builtin_bit_cast(uint32_t, b2) | __builtin_bit_cast(uint32_t, b3)) & 0x80008000u;
+    nonfinite = signs != 0 || top == 0x7fff;
+    return top < 0x3ff ? 0u : (uint32_t)(top - 0x3ff);
 }
 
 // SiLU(g) * u (src/npu.rs:1202-1208: g / (1 + e^-g) * u) with the hardware exp2 and

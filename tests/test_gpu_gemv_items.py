@@ -205,3 +205,76 @@ def test_fused_rows_three_groups_per_thread(oracle, bits, M):
     check_outputs(oracle, out, expect, False, torch.float16)
     w.close()
     ws.close()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K,N,swiglu", [(2560, 6144, False), (4096, 2560, False), (2560, 2 * 9728, True),
+                                        (9728, 2560, False)])
+@pytest.mark.parametrize("M", [5, 6, 7, 8])
+def test_fused_rows_five_to_eight(oracle, bits, K, N, swiglu, M):
+    """5..8 rows quantize inside the GEMV in the 8-row instances (8 waves, one activation
+    group per thread per row) wherever a row holds at most 512 groups (K <= 4096: the qkv, o
+    and gate_up shapes), equal bit for bit to the separate-quantize launch and to the
+    oracle; K = 9728 (down) takes the separate launch."""
+    ws = ql.Workspace(8, K, N)
+    codes = synth.codes(N, K, bits, 340 + bits + K % 13 + M).numpy()
+    sc = synth.scales(N, bits, 341 + bits).numpy()
+    w = make_weights(bits, codes, sc)
+    A = synth.activations(M, K, seed=342 + M, dist="student_t3")
+    flags = ql.QLIN_SWIGLU if swiglu else 0
+    fused = K <= 4096
+    for dt in (torch.float16, torch.float32):
+        a = A.to(DEV).to(dt)
+        pl = ql.plan(ws, w, a, flags)
+        assert pl["path"] == (ql.QLIN_PATH_GEMV_FUSED if fused else ql.QLIN_PATH_GEMV), pl
+        if fused:
+            assert pl["waves"] == 8, pl
+        out = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags)
+        sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags | ql.QLIN_NO_FUSED_QUANT)
+        torch.cuda.synchronize()
+        assert np.array_equal(f16_bits(out), f16_bits(sep)), dt
+        check_outputs(oracle, out, oracle_linear(oracle, A, codes, sc, swiglu), swiglu, torch.float16)
+    w.close()
+    ws.close()
+
+
+@pytest.mark.parametrize("K", [2560, 4096, 9728])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8])
+def test_fused_nonfinite_rows_match_separate(oracle, M, K):
+    """Rows holding NaN and Inf through the fused prologue (whichever instance the plan
+    takes) equal the separate quantize launch, which equals the oracle: the row maximum is
+    the reference's fold of f32::max over |x| (src/npu.rs:1101-1106), NaN ignored and Inf
+    kept.  Row 0 holds a NaN in the same 8-value group as its largest value, so dropping
+    that group from the maximum would change the row's scale; with two or more rows the last
+    row holds an Inf (scale Inf, every output of the row NaN).  fp16 and f32 rows; the
+    status word reports the non-finite input on both paths."""
+    N = 2560
+    ws = ql.Workspace(8, K, N)
+    codes = synth.codes(N, K, 4, 350 + M + K % 17).numpy()
+    sc = synth.scales(N, 4, 351).numpy()
+    w = make_weights(4, codes, sc)
+    A = synth.activations(M, K, seed=352 + M).float()
+    A[0, 43] = float("nan")
+    A[0, 42] = 3000.0  # the row's largest value, in the NaN's group (columns 40..47)
+    if M >= 2:
+        A[M - 1, 3] = float("inf")
+    q_ref, s_ref, nbad = oracle.quantize(A.numpy())
+    assert nbad == min(M, 2)
+    assert s_ref[0] == np.float32(np.float32(3000.0) / np.float32(127.0))
+    assert M == 1 or s_ref[M - 1] == np.inf
+    for dt in (torch.float16, torch.float32):
+        a = A.to(dt).to(DEV)
+        ws.status(clear=True)
+        out = ql.run(ws, w, a, out_dtype=torch.float32)
+        assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
+        sep = ql.run(ws, w, a, out_dtype=torch.float32, flags=ql.QLIN_NO_FUSED_QUANT)
+        assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
+        q, s = ql.quantize(a, ldq=w.K_padded)
+        torch.cuda.synchronize()
+        assert np.array_equal(q.cpu().numpy()[:, :K], q_ref)
+        assert np.array_equal(s.cpu().numpy(), s_ref)
+        o, e = out.cpu().numpy(), sep.cpu().numpy()
+        assert np.array_equal(o, e, equal_nan=True), (dt, np.argwhere(~((o == e) | (np.isnan(o) & np.isnan(e))))[:3])
+        assert np.isfinite(o[0]).all() and np.isnan(o[M - 1]).all() == (M >= 2)
+    w.close()
+    ws.close()

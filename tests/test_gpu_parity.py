@@ -341,10 +341,11 @@ def test_nonfinite_activation_sets_status(ws):
 
 
 @pytest.mark.parametrize("norm", [False, True])
-@pytest.mark.parametrize("M", [1, 4, 40, 1030])
+@pytest.mark.parametrize("M", [1, 4, 6, 40, 1030])
 def test_nonfinite_row_sets_status_every_path(ws, M, norm):
     """One Inf in the last activation row sets the sticky error word on every path: the
-    fused-quantization GEMV (1 and 4 rows), the quantize launch before the GEMM (40 rows) and
+    fused-quantization GEMV (1, 4 and, without RMSNorm, 6 rows; 6 rows with RMSNorm take the
+    separate quantize launch), the quantize launch before the GEMM (40 rows) and
     the many-rows quantize kernels (1030 rows), with and without RMSNorm; a clean run after it
     leaves the word clear."""
     K, N = 2560, 256
