@@ -246,8 +246,9 @@ def test_fused_nonfinite_rows_match_separate(oracle, M, K):
     the reference's fold of f32::max over |x| (src/npu.rs:1101-1106), NaN ignored and Inf
     kept.  Row 0 holds a NaN in the same 8-value group as its largest value, so dropping
     that group from the maximum would change the row's scale; with two or more rows the last
-    row holds an Inf (scale Inf, every output of the row NaN).  fp16 and f32 rows; the
-    status word reports the non-finite input on both paths."""
+    row holds an Inf (scale Inf, every output of the row NaN).  fp16 and f32 rows, with and
+    without RMSNorm (which turns a NaN or Inf row into NaN values throughout: maximum 0, scale
+    1, every code 0); the status word reports the non-finite input on both paths."""
     N = 2560
     ws = ql.Workspace(8, K, N)
     codes = synth.codes(N, K, 4, 350 + M + K % 17).numpy()
@@ -258,23 +259,29 @@ def test_fused_nonfinite_rows_match_separate(oracle, M, K):
     A[0, 42] = 3000.0  # the row's largest value, in the NaN's group (columns 40..47)
     if M >= 2:
         A[M - 1, 3] = float("inf")
-    q_ref, s_ref, nbad = oracle.quantize(A.numpy())
-    assert nbad == min(M, 2)
-    assert s_ref[0] == np.float32(np.float32(3000.0) / np.float32(127.0))
-    assert M == 1 or s_ref[M - 1] == np.inf
-    for dt in (torch.float16, torch.float32):
-        a = A.to(dt).to(DEV)
-        ws.status(clear=True)
-        out = ql.run(ws, w, a, out_dtype=torch.float32)
-        assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
-        sep = ql.run(ws, w, a, out_dtype=torch.float32, flags=ql.QLIN_NO_FUSED_QUANT)
-        assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
-        q, s = ql.quantize(a, ldq=w.K_padded)
-        torch.cuda.synchronize()
-        assert np.array_equal(q.cpu().numpy()[:, :K], q_ref)
-        assert np.array_equal(s.cpu().numpy(), s_ref)
-        o, e = out.cpu().numpy(), sep.cpu().numpy()
-        assert np.array_equal(o, e, equal_nan=True), (dt, np.argwhere(~((o == e) | (np.isnan(o) & np.isnan(e))))[:3])
-        assert np.isfinite(o[0]).all() and np.isnan(o[M - 1]).all() == (M >= 2)
+    gam = synth.gamma(K, seed=353)
+    for norm in (False, True):
+        x = oracle.rmsnorm(A.numpy(), gam.numpy(), 1e-6, "neon16") if norm else A.numpy()
+        q_ref, s_ref, nbad = oracle.quantize(x)
+        assert nbad == min(M, 2)
+        if not norm:
+            assert s_ref[0] == np.float32(np.float32(3000.0) / np.float32(127.0))
+            assert M == 1 or s_ref[M - 1] == np.inf
+        g = gam.to(DEV) if norm else None
+        for dt in (torch.float16, torch.float32):
+            a = A.to(dt).to(DEV)
+            ws.status(clear=True)
+            out = ql.run(ws, w, a, out_dtype=torch.float32, gamma=g, eps=1e-6)
+            assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
+            sep = ql.run(ws, w, a, out_dtype=torch.float32, flags=ql.QLIN_NO_FUSED_QUANT, gamma=g, eps=1e-6)
+            assert ws.status(clear=True) == ql._lib.QLIN_ERR_NONFINITE
+            q, s = ql.quantize(a, ldq=w.K_padded, gamma=g, eps=1e-6)
+            torch.cuda.synchronize()
+            assert np.array_equal(q.cpu().numpy()[:, :K], q_ref), (norm, dt)
+            assert np.array_equal(s.cpu().numpy(), s_ref), (norm, dt)
+            o, e = out.cpu().numpy(), sep.cpu().numpy()
+            assert np.array_equal(o, e, equal_nan=True), (norm, dt, np.argwhere(~((o == e) | (np.isnan(o) & np.isnan(e))))[:3])
+            if not norm:
+                assert np.isfinite(o[0]).all() and np.isnan(o[M - 1]).all() == (M >= 2)
     w.close()
     ws.close()
