@@ -209,7 +209,7 @@ def test_fused_rows_three_groups_per_thread(oracle, bits, M):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("K,N,swiglu", [(2560, 6144, False), (4096, 2560, False), (2560, 2 * 9728, True),
-                                        (9728, 2560, False)])
+                                        (9728, 2560, False), (1024, 2 * 1000, True), (512, 600, False)])
 @pytest.mark.parametrize("M", [5, 6, 7, 8])
 def test_fused_rows_five_to_eight(oracle, bits, K, N, swiglu, M):
     """5..8 rows quantize inside the GEMV in the 8-row instances (8 waves, one activation
