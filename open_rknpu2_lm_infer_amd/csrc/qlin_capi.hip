@@ -242,10 +242,16 @@ int upload_scales(qlin_weights* x, const float* scales, hipMemcpyKind kind, hipS
     return QLIN_OK;
 }
 
+// Whether the decode GEMV takes the rows (else quantize + GEMM).  17..32 rows go through
+// the GEMV's two row blocks where it measured faster than the GEMM: every shape up to 20
+// rows, and up to 32 for outputs of at most 4096 channels, whose GEMM grid is a few wide
+// tiles split along K (W4 layer, µs per linear with its quantize launch, GEMM -> GEMV: o /
+// down at 17 rows 14.3 / 18.9 -> 9.4 / 14.0, at 32 rows 14.4 / 19.1 -> 10.6 / 17.5; qkv /
+// gate_up at 17 rows 14.7 / 16.4 -> 14.1 / 14.5, at 32 rows 14.8 / 16.5 -> 16.6 / 17.8).
 bool gemv_ok(const qlin_workspace* ws, const qlin_weights* w, int rows) {
     (void)ws;
-    (void)w;
-    return rows <= kGemvMaxRows;
+    if (rows <= kGemvMaxRows) return true;
+    return rows <= kGemvMaxRowsWide && (rows <= 20 || w->N <= 4096);
 }
 
 }  // namespace
@@ -577,6 +583,9 @@ GemvPlan plan_gemv(const qlin_workspace* ws, const qlin_weights* w, int rows, bo
     } else if (fused && !gemv_can_fuse(rows, w->K, waves, norm)) {
         waves = 0;
     }
+    // 17..32 quantized rows: at most 8 waves (1024-thread workgroups would spill the two row
+    // blocks' registers)
+    if (!fused && rows > kGemvMaxRows && waves > 8) waves = 8;
     g.waves = waves;
     // More items than CUs with the quantization fused: one workgroup per CU (at most four
     // items each), so each CU quantizes the rows once.  On rows quantized beforehand, only

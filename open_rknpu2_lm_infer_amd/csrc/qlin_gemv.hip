@@ -22,7 +22,8 @@ template __global__ void gemv_kernel<8, false, 1, false, 16, 4, kTwoGroupRegs>(G
 template __global__ void gemv_items_kernel<4, true, 1, true, 8, 4, kOneGroupRegs>(GemvParams);
 
 size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm, int items) {
-    if (items <= 1) {
+    const size_t rb = !fused && M > kGemvMaxRows ? 2 : 1;  // row blocks: 17..32 take the items kernel
+    if (items <= 1 && rb == 1) {
         // gemv_kernel: the reduction area reuses the activation area
         size_t a = fused ? (size_t)(M + 1) * (Kp + 16) : 0;
         if (norm) a = std::max(a, (size_t)M * K * sizeof(float));
@@ -30,7 +31,7 @@ size_t gemv_lds_bytes_for(int M, int Kp, int K, int waves, bool fused, bool norm
     }
     const size_t rows = fused ? (M == 1 ? 1 : M <= kFusedRowsWide ? 4 : 8) : kGemvMaxRows;  // rows leaving the matrix core
     const size_t live = 16 * ((rows + 3) / 4), regs = rows < 4 ? rows : 4;
-    const size_t red = (size_t)items * 2 * waves * live * regs * sizeof(int);
+    const size_t red = (size_t)(items > 1 ? items : 1) * rb * 2 * waves * live * regs * sizeof(int);
     return gemv_red_offset(M, Kp, K, fused, norm) + red;
 }
 
@@ -73,9 +74,37 @@ static hipError_t launch_m(const GemvParams& p, int waves, size_t lds, hipStream
                 : launch_w<BITS, SWIGLU, MODE, false, 4>(p, waves, lds, st);
 }
 
+// 17..32 quantized rows: two row blocks per weight fragment, always the items kernel (its
+// partial sums of both blocks meet in LDS; one item per workgroup unless the plan groups them)
+template <int BITS, bool SWIGLU, int WAVES>
+static hipError_t launch_rows2_w(const GemvParams& p, size_t lds, hipStream_t st) {
+    const int groups = gemv_items(p);
+    const dim3 grid(p.grid > 0 && p.grid < groups ? p.grid : groups);
+    const void* f = reinterpret_cast<const void*>(&gemv_items_kernel<BITS, SWIGLU, 0, false, WAVES, 2, 0>);
+    if (lds > 64 * 1024) {
+        static const hipError_t a = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
+        if (a != hipSuccess) return a;
+    }
+    hipLaunchKernelGGL((gemv_items_kernel<BITS, SWIGLU, 0, false, WAVES, 2, 0>), grid, dim3(64 * WAVES), lds, st, p);
+    return hipGetLastError();
+}
+
+template <int BITS, bool SWIGLU>
+static hipError_t launch_rows2(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
+    switch (waves) {
+        case 4: return launch_rows2_w<BITS, SWIGLU, 4>(p, lds, st);
+        case 8: return launch_rows2_w<BITS, SWIGLU, 8>(p, lds, st);
+        default: return hipErrorInvalidValue;  // 1024-thread workgroups would spill both blocks' buffers
+    }
+}
+
 template <int BITS, bool SWIGLU>
 static hipError_t launch_b(const GemvParams& p, int waves, size_t lds, hipStream_t st) {
-    if (!p.A) return launch_w<BITS, SWIGLU, 0, false, 1>(p, waves, lds, st);
+    if (!p.A) {
+        if (p.M > kGemvMaxRowsWide) return hipErrorInvalidValue;
+        if (p.M > kGemvMaxRows) return launch_rows2<BITS, SWIGLU>(p, waves, lds, st);
+        return launch_w<BITS, SWIGLU, 0, false, 1>(p, waves, lds, st);
+    }
     return p.a_f16 ? launch_m<BITS, SWIGLU, 1>(p, waves, lds, st) : launch_m<BITS, SWIGLU, 2>(p, waves, lds, st);
 }
 

@@ -97,10 +97,11 @@ __device__ __forceinline__ void a_from_global(v4i a[4], const int8_t* qrow, bool
 
 // Registers of BATCH wave steps: weights (gate, up) and, when the rows arrive
 // quantized, the matching A operands.
-template <int BATCH, bool FUSED>
+template <int BATCH, bool FUSED, int RB = 1>
 struct StepBuf {
     v4i bg[BATCH][2], bu[BATCH][2];
     v4i a[FUSED ? 1 : BATCH][4];
+    v4i a2[!FUSED && RB > 1 ? BATCH : 1][4];  // rows 16..31 (two row blocks of quantized rows)
 };
 
 // Issues the loads of one batch with no branches: steps past the end re-read the
@@ -163,10 +164,11 @@ struct GemvPos {
 // re-read the last one (an L2 hit), so the compiler can count outstanding loads
 // exactly and never has to wait for more than it consumes.  In the quantized mode
 // the A loads of a position are issued before its weights.
-template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH>
-__device__ __forceinline__ void load_batch_items(StepBuf<BATCH, FUSED>& s, const GemvParams& p, GemvPos& pos, int& c,
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH, int RB = 1>
+__device__ __forceinline__ void load_batch_items(StepBuf<BATCH, FUSED, RB>& s, const GemvParams& p, GemvPos& pos, int& c,
                                            int total, GemvPos last, const uint8_t* wlane, int64_t up_off,
-                                           const int8_t* qrow, bool live, int steps, int lrow, int ncols) {
+                                           const int8_t* qrow, bool live, int steps, int lrow, int ncols,
+                                           const int8_t* qrow2 = nullptr, bool live2 = false) {
     constexpr int KS = BITS == 4 ? 256 : 128;
 #pragma unroll
     for (int i = 0; i < BATCH; ++i) {
@@ -175,6 +177,7 @@ __device__ __forceinline__ void load_batch_items(StepBuf<BATCH, FUSED>& s, const
         const int row = min(p.iw * ((int)blockIdx.x + q.j * (int)gridDim.x) + lrow, ncols - 1);
         const uint8_t* wg = wlane + (int64_t)row * p.wrow + (int64_t)q.t * 128;
         if constexpr (!FUSED) a_from_global<BITS>(s.a[i], qrow + q.t * KS, live);
+        if constexpr (!FUSED && RB > 1) a_from_global<BITS>(s.a2[i], qrow2 + q.t * KS, live2);
         s.bg[i][0] = ld16(wg);
         s.bg[i][1] = ld16(wg + 64);
         if constexpr (SWIGLU) {
@@ -204,15 +207,24 @@ __device__ __forceinline__ void gemv_flush(int* red, int j, int wave, int lane, 
 
 // MFMAs of BATCH positions; cj is the item whose sums ag / au hold.  Moving to a later
 // item flushes them (and zero sums for items this wave has no step of).
-template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH, int LIVE, int REGS>
-__device__ __forceinline__ void compute_batch_items(v4i& ag, v4i& au, const StepBuf<BATCH, FUSED>& s, const uint8_t* arow,
+template <int BITS, bool SWIGLU, bool FUSED, int WAVES, int BATCH, int LIVE, int REGS, int RB = 1>
+__device__ __forceinline__ void compute_batch_items(v4i& ag, v4i& au, const StepBuf<BATCH, FUSED, RB>& s, const uint8_t* arow,
                                               GemvPos& pos, int& c, int total, int& cj, int* red, int wave, int lane,
-                                              int steps) {
+                                              int steps, v4i* ag2 = nullptr, v4i* au2 = nullptr) {
     constexpr int KS = BITS == 4 ? 256 : 128;
 #pragma unroll
     for (int i = 0; i < BATCH; ++i) {
         if (c < total) {
-            while (cj < pos.j) gemv_flush<SWIGLU, WAVES, LIVE, REGS>(red, cj++, wave, lane, ag, au);
+            if constexpr (RB > 1) {
+                // item j's row blocks take the sum slots 2j and 2j + 1
+                while (cj < pos.j) {
+                    gemv_flush<SWIGLU, WAVES, LIVE, REGS>(red, 2 * cj, wave, lane, ag, au);
+                    gemv_flush<SWIGLU, WAVES, LIVE, REGS>(red, 2 * cj + 1, wave, lane, *ag2, *au2);
+                    ++cj;
+                }
+            } else {
+                while (cj < pos.j) gemv_flush<SWIGLU, WAVES, LIVE, REGS>(red, cj++, wave, lane, ag, au);
+            }
             v4i a[4];
             if constexpr (FUSED) {
                 a_from_lds<BITS>(a, arow + pos.t * KS);
@@ -222,6 +234,13 @@ __device__ __forceinline__ void compute_batch_items(v4i& ag, v4i& au, const Step
             }
             mfma_step<BITS>(ag, s.bg[i], a);
             if constexpr (SWIGLU) mfma_step<BITS>(au, s.bu[i], a);
+            if constexpr (!FUSED && RB > 1) {
+                v4i a2[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a2[j] = s.a2[i][j];
+                mfma_step<BITS>(*ag2, s.bg[i], a2);
+                if constexpr (SWIGLU) mfma_step<BITS>(*au2, s.bu[i], a2);
+            }
             pos.advance(WAVES, steps);
             ++c;
         }
@@ -996,14 +1015,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     constexpr bool FUSED = MODE != 0;
     constexpr int NT = 64 * WAVES;
     constexpr int KS = BITS == 4 ? 256 : 128;
-    constexpr int BATCH = GemvCfg<WAVES, FUSED>::BATCH;
+    // (two row blocks of quantized rows: one step per batch, or the buffers would spill)
+    constexpr int BATCH = !FUSED && MR > 1 ? 1 : GemvCfg<WAVES, FUSED>::BATCH;
     constexpr int XR = XW > 0 ? XW
                        : XW < 0 ? MR * -XW
                        : NORM   ? (MR > 1 ? kNormRowsRegs : GemvCfg<WAVES, FUSED>::XREGS_NORM)
                                 : GemvCfg<WAVES, FUSED>::XREGS;
     constexpr int ROWS = FUSED ? MR : kGemvMaxRows;  // rows whose sums leave the matrix core
+    // quantized rows (MODE 0) in MR blocks of 16: 17..32 rows take two blocks, each weight
+    // fragment feeding one MFMA per block
+    constexpr int RB = FUSED ? 1 : MR;
+    static_assert(RB == 1 || RB == 2, "one or two row blocks");
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_rows[kGemvMaxRows];
+    __shared__ float s_rows[kGemvMaxRows * RB];
     gemv_fetch_params(p);
     __shared__ float s_inv[kFusedMaxRows];
     __shared__ float s_red[kFusedMaxRows][WAVES];  // wave maxima per row (0 from waves owning no group)
@@ -1084,7 +1108,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     const uint8_t* wlane = p.W + (lane >> 4) * 16;
     const int64_t up_off = SWIGLU ? (int64_t)Nh * p.wrow : 0;
     const int8_t* qrow = FUSED ? nullptr : p.q + (int64_t)m_src * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16);
-    StepBuf<BATCH, FUSED> b0, b1;
+    const bool live2 = RB > 1 && 16 + m_lane < p.M;
+    const int8_t* qrow2 = RB > 1 ? p.q + (int64_t)min(16 + m_lane, p.M - 1) * p.ldq + (lane >> 4) * (BITS == 4 ? 32 : 16)
+                                 : nullptr;
+    StepBuf<BATCH, FUSED, RB> b0, b1;
     // next position to load, and the last one of the sequence (item 0, step 0 for a
     // wave without steps, so that its loads below stay in bounds)
     const int f_last = wave + (total - 1) * WAVES;
@@ -1098,10 +1125,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     // us).  Unconditional, so that the waits for the activation loads above count
     // exactly these loads after them.
     constexpr int PRE = WAVES <= 8 && !SWIGLU ? 2 : 1;
-    load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
+    load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
     if constexpr (PRE == 2) {
         asm volatile("" ::: "memory");  // keep batch 0's loads ahead of batch 1's
-        load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
+        load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
     }
 
     // ---- 3. prologue: per-token scale and quantized rows in LDS ------------------
@@ -1280,36 +1307,45 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_items_kernel(GemvParams p) {
     int* red = reinterpret_cast<int*>(smem + gemv_red_offset(p.M, p.Kp, p.K, FUSED, NORM));
     const uint8_t* arow = lds_a + (live ? m_lane : p.M) * astride + (lane >> 4) * (BITS == 4 ? 32 : 16);
     v4i ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
+    v4i ag2 = {0, 0, 0, 0}, au2 = {0, 0, 0, 0};  // the second row block
     GemvPos cpos{wave / steps, wave % steps};  // next position to multiply
     int cc = 0, cj = 0;
     while (cc < total) {
         if (PRE == 1 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
-        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b0, arow, cpos, cc, total, cj, red,
-                                                                           wave, lane, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
+        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS, RB>(ag, au, b0, arow, cpos, cc, total, cj,
+                                                                               red, wave, lane, steps, &ag2, &au2);
         if (PRE == 2 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
         if (cc >= total) break;
         if (PRE == 1 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
-        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS>(ag, au, b1, arow, cpos, cc, total, cj, red,
-                                                                           wave, lane, steps);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b0, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
+        compute_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, LIVE_LANES, REGS, RB>(ag, au, b1, arow, cpos, cc, total, cj,
+                                                                               red, wave, lane, steps, &ag2, &au2);
         if (PRE == 2 && lc < total)
-            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols);
+            load_batch_items<BITS, SWIGLU, FUSED, WAVES, BATCH, RB>(b1, p, lpos, lc, total, last, wlane, up_off, qrow, live, steps, lrow, ncols, qrow2, live2);
     }
-    while (cj < n_items) gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, cj++, wave, lane, ag, au);
+    if constexpr (RB > 1) {
+        for (; cj < n_items; ++cj) {
+            gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, 2 * cj, wave, lane, ag, au);
+            gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, 2 * cj + 1, wave, lane, ag2, au2);
+        }
+    } else {
+        while (cj < n_items) gemv_flush<SWIGLU, WAVES, LIVE_LANES, REGS>(red, cj++, wave, lane, ag, au);
+    }
 
     // ---- 5. cross-wave reduction and epilogue ------------------------------------
     lds_barrier();
     for (int o = tid; o < n_items * 16 * p.M; o += NT) {
         const int jj = o / (16 * p.M), rem = o - jj * 16 * p.M;
         const int m = rem >> 4, n = rem & 15;
-        const int src = (16 * (m >> 2) + n) * REGS + (m & 3);
+        const int mb = RB > 1 ? m & 15 : m, slot = RB > 1 ? 2 * jj + (m >> 4) : jj;  // row in its block, sum slot
+        const int src = (16 * (mb >> 2) + n) * REGS + (mb & 3);
         int vg = 0, vu = 0;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
-            vg += red[((jj * 2) * WAVES + w) * LIVE_LANES * REGS + src];
-            if constexpr (SWIGLU) vu += red[((jj * 2 + 1) * WAVES + w) * LIVE_LANES * REGS + src];
+            vg += red[((slot * 2) * WAVES + w) * LIVE_LANES * REGS + src];
+            if constexpr (SWIGLU) vu += red[((slot * 2 + 1) * WAVES + w) * LIVE_LANES * REGS + src];
         }
         const int r0 = p.iw * ((int)blockIdx.x + jj * (int)gridDim.x);
         if (n >= p.iw) continue;  // a re-read row, not an output

@@ -19,7 +19,8 @@ namespace qlin {
 constexpr int kKAlign = 256;  // Kp alignment (one GEMV wave step of W4 spans 256 k)
 constexpr int kNAlign = 64;   // Np alignment
 constexpr int kMaxK = 131072; // int32 accumulators cannot overflow below this K (W4 codes x16)
-constexpr int kGemvMaxRows = 16;
+constexpr int kGemvMaxRows = 16;      // rows of one matrix-core block of the decode GEMV
+constexpr int kGemvMaxRowsWide = 32;  // rows the GEMV takes quantized: two blocks of 16
 // Rows a fused GEMV prologue quantizes: up to 4 in every instance, 5..8 in the 8-row
 // instances (512-thread workgroups, one activation group per thread per row, no RMSNorm).
 constexpr int kFusedMaxRows = 8;

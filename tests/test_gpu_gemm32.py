@@ -33,7 +33,7 @@ def cfg_ws(cfg, rows, K, N, splits=None):
 
 # every (configuration, bits) pair the kernel has: configuration 3 exists for W4 only
 @pytest.mark.parametrize("cfg,bits", [(c, b) for b in (4, 8) for c in ((0, 1, 2, 3) if b == 4 else (0, 1, 2))])
-@pytest.mark.parametrize("K,N,M,splits", [(2560, 1024, 300, None), (4096, 640, 17, 3), (1024, 2000, 513, 2)])
+@pytest.mark.parametrize("K,N,M,splits", [(2560, 1024, 300, None), (4096, 640, 33, 3), (1024, 2000, 513, 2)])
 def test_gemm32_configs_match_oracle(oracle, cfg, bits, K, N, M, splits):
     codes = synth.codes(N, K, bits, 600 + cfg + K % 7 + bits).numpy()
     sc = synth.scales(N, bits, 601 + bits).numpy()

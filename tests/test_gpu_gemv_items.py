@@ -285,3 +285,36 @@ def test_fused_nonfinite_rows_match_separate(oracle, M, K):
                 assert np.isfinite(o[0]).all() and np.isnan(o[M - 1]).all() == (M >= 2)
     w.close()
     ws.close()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K,N,swiglu", [(2560, 6144, False), (2560, 2 * 9728, True), (4096, 2560, False),
+                                        (9728, 2560, False), (1024, 2 * 1000, True)])
+@pytest.mark.parametrize("M", [17, 20, 31, 32])
+def test_gemv_two_row_blocks(oracle, bits, K, N, swiglu, M):
+    """17..32 rows, quantized by a separate launch, take the GEMV with two 16-row blocks per
+    weight fragment (the items kernel, at most 8 waves) up to 20 rows, and up to 32 rows for
+    at most 4096 output channels; the GEMM otherwise.  Against the oracle (plain fp16
+    bit-exact, SiLU-gate within 1e-3), fp16 and f32 rows, and on the GEMV bit for bit with
+    every item in a workgroup of its own."""
+    ws = ql.Workspace(32, K, N)
+    codes = synth.codes(N, K, bits, 360 + bits + K % 13 + M).numpy()
+    sc = synth.scales(N, bits, 361 + bits).numpy()
+    w = make_weights(bits, codes, sc)
+    A = synth.activations(M, K, seed=362 + M, dist="student_t3")
+    flags = ql.QLIN_SWIGLU if swiglu else 0
+    expect = oracle_linear(oracle, A, codes, sc, swiglu)
+    for dt in (torch.float16, torch.float32):
+        a = A.to(DEV).to(dt)
+        pl = ql.plan(ws, w, a, flags)
+        if M <= 20 or N <= 4096:
+            assert pl["path"] == ql.QLIN_PATH_GEMV and pl["waves"] <= 8, pl
+            out, ref = run_both(ws, w, a, out_dtype=torch.float16, flags=flags)
+            torch.cuda.synchronize()
+            assert np.array_equal(f16_bits(out), f16_bits(ref)), dt
+        else:
+            assert pl["path"] == ql.QLIN_PATH_GEMM, pl
+            out = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags)
+        check_outputs(oracle, out, expect, swiglu, torch.float16)
+    w.close()
+    ws.close()

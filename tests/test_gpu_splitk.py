@@ -35,7 +35,7 @@ def split_ws(rows, K, N, splits):
 # (M, K, N, splits, plain tiles of 128 x 128): 8 and 24 tiles keep a tile's splits on one
 # XCD; 10 and 20 tiles (grids of 30 and 60) do not
 SHAPES = [(256, 2048, 512, 2, 8), (256, 2048, 512, 4, 8), (200, 3072, 1536, 3, 24), (130, 4096, 640, 3, 10),
-          (17, 9728, 2560, 3, 20)]
+          (33, 9728, 2560, 3, 20)]
 
 
 @pytest.mark.parametrize("bits", [4, 8])
