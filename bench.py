@@ -431,10 +431,11 @@ def main():
     dom = per_kernel["gate_up"]
 
     # ---------------------------------------------------------------- decode at M = 2, 4, 8 rows
-    # (the speculative-verify batch of 1 + up to 7 draft tokens, src/model/speculation.rs:36,51):
-    # the same layer step and per-projection rotation as M = 1
+    # (the speculative-verify batch of 1 + up to 7 draft tokens, src/model/speculation.rs:36,51),
+    # and 16 / 32 rows (the GEMV's one and two row blocks of quantized rows): the same layer
+    # step and per-projection rotation as M = 1
     decode_rows = {}
-    for M in (2, 4, 8):
+    for M in (2, 4, 8, 16, 32):
         acts_m = [synth.activations(M, K, seed=synth.linear_seed(0, p) + 10 + M, device=dev)
                   for p, (_, K, _) in enumerate(synth.LAYER)]
         outs_m = [torch.empty((M, N // 2 if name == "gate_up" else N), dtype=torch.float16, device=dev)
