@@ -63,7 +63,7 @@ def test_tune_search_keeps_outputs(tmp_path):
     ql.tune_clear()
     ws = ql.Workspace(512, 9728, 19456)
     cases = [(4, 2560, 19456, 1, ql.QLIN_SWIGLU), (8, 4096, 2560, 8, 0), (4, 9728, 2560, 512, 0),
-             (8, 2560, 6144, 300, 0)]
+             (8, 2560, 6144, 300, 0), (4, 4096, 2560, 24, 0)]
     for i, (bits, K, N, M, fl) in enumerate(cases):
         packed, _, sc = synth.make_linear(N, K, bits, 970 + i, device="cuda:0")
         w = ql.Weights.from_packed_device(bits, K, N, packed, sc)
