@@ -42,6 +42,7 @@ def weights(bits, K, N, seed):
     (2560, 6144, False, True, (1024, 17)),  # GEMM after RMSNorm-quantize
     (2560, 2000, True, False, (300, 2)),    # SiLU-gate at N % 64 != 0
     (2560, 6144, False, False, (8, 5)),     # 5..8-row fused decode GEMV
+    (4096, 2560, False, False, (24, 20)),   # 17..32 quantized rows: the GEMV's two row blocks
 ])
 def test_noalloc_matches_workspace_entry(bits, K, N, swiglu, norm, rows):
     w = weights(bits, K, N, 800 + K % 97 + N % 89 + bits)
