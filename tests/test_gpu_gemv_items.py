@@ -318,3 +318,36 @@ def test_gemv_two_row_blocks(oracle, bits, K, N, swiglu, M):
         check_outputs(oracle, out, expect, swiglu, torch.float16)
     w.close()
     ws.close()
+
+
+@pytest.mark.parametrize("K", [2560, 4096])
+@pytest.mark.parametrize("rne", [False, True])
+def test_fused_edge_rows_match_separate(oracle, K, rne):
+    """Rows whose x * (1/s) land exactly on k + 0.5 (the rounding ties), an all-zero row
+    (s = 1) and a row holding only an fp16 subnormal, through the fused prologue one row at a
+    time, as 3 rows and as 6 rows (with 3 ordinary rows: the 5..8-row instances), in both
+    rounding modes: every output bit for bit equal to the separate quantize launch and to the
+    oracle (plain fp16 outputs)."""
+    from tests.test_gpu_parity import tie_rows
+    N = 2560
+    ws = ql.Workspace(8, K, N)
+    codes = synth.codes(N, K, 4, 370 + K % 7 + rne).numpy()
+    sc = synth.scales(N, 4, 371).numpy()
+    w = make_weights(4, codes, sc)
+    edge = torch.from_numpy(tie_rows(K))
+    rows = [edge[i:i + 1] for i in range(3)] + [edge, torch.cat([edge, synth.activations(3, K, seed=372).float()], 0)]
+    flags = ql.QLIN_ROUND_HALF_EVEN if rne else 0
+    mode = oracle.ROUND_EVEN if rne else oracle.ROUND_AWAY
+    for A in rows:
+        M = A.shape[0]
+        for dt in (torch.float16, torch.float32):
+            expect = oracle_linear(oracle, A.to(dt), codes, sc, False, round_mode=mode)  # the rows as the GPU sees them
+            a = A.to(dt).to(DEV)
+            assert ql.plan(ws, w, a, flags)["path"] == ql.QLIN_PATH_GEMV_FUSED, M
+            out = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags)
+            sep = ql.run(ws, w, a, out_dtype=torch.float16, flags=flags | ql.QLIN_NO_FUSED_QUANT)
+            torch.cuda.synchronize()
+            assert np.array_equal(f16_bits(out), f16_bits(sep)), (M, dt)
+            check_outputs(oracle, out, expect, False, torch.float16)
+    w.close()
+    ws.close()
