@@ -29,7 +29,7 @@ def ws():
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M", [1, 4, 16, 17, 512])
+@pytest.mark.parametrize("M", [1, 4, 6, 16, 17, 32, 512])
 def test_residual_linear_bitexact(oracle, ws, bits, M):
     K, N = 4096, 2560  # the o projection's shape
     codes = synth.codes(N, K, bits, 70 + bits).numpy()
